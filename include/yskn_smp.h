@@ -1,0 +1,205 @@
+/*
+ * yskn_smp.h -- C ABI of the MI355X (gfx950) sampling library.
+ *
+ * The per-step logits -> token path of YASAKANI as a thin C ABI in the shape
+ * of the reference's include/yskn_abi.h: an opaque handle, int status
+ * (0 = success, negative = failure), a thread-local last-error string,
+ * caller-owned device buffers and an explicit HIP stream. No C++ or torch
+ * types cross this boundary.
+ *
+ * Semantics follow the reference's scalar specification
+ * (crates/yskn-ref/src/output_head_sampler.rs) bit for bit: selected token ids,
+ * top-k index sets, argmax and accepted-draft counts are identical to it on the
+ * same logits, parameters and prediction positions.
+ *
+ * Threading: a handle is used by one host thread at a time (the reference's
+ * "one engine per thread", crates/yskn-cli/src/lib.rs:1). Calls on one handle
+ * must be issued to one stream or otherwise ordered: the handle's workspace is
+ * shared by its calls.
+ */
+#ifndef YSKN_SMP_H
+#define YSKN_SMP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- status codes --------------------------------------------------------
+ * The reference returns Result<_, Error> (crates/yskn-ref/src/lib.rs:37-45)
+ * and, at its C ABI, 0 / -1 plus yskn_last_error() (src/c_api.cpp:11-14). */
+#define YSKN_SMP_OK 0
+#define YSKN_SMP_EINVAL (-1)     /* Error::InvalidInput */
+#define YSKN_SMP_ENONFINITE (-2) /* Error::NonFinite("logits") */
+#define YSKN_SMP_ERANGE (-3)     /* vocabulary or rows beyond the handle's limits */
+#define YSKN_SMP_EDEVICE (-4)    /* HIP runtime failure */
+
+/* ---- handle flags ------------------------------------------------------- */
+/* Lift the reference's 1..=20 top_k cap (output_head_sampler.rs:68-72) to
+ * 1..=V, with top_k = 0 meaning "disabled" (k = V). Without this flag top_k
+ * outside 1..=min(20, V) is rejected exactly like the reference. */
+#define YSKN_SMP_FLAG_EXTENDED_TOP_K 0x1u
+/* Test hook: route every row through the exact large-candidate ("dense")
+ * path even when the compact path would serve it. Results are identical. */
+#define YSKN_SMP_FLAG_FORCE_DENSE 0x2u
+
+/* ---- logits element type ------------------------------------------------ */
+#define YSKN_SMP_F32 0
+#define YSKN_SMP_BF16 1 /* widened exactly: bits << 16 (crates/yskn-format/src/floats.rs:55-57) */
+
+/* ---- sampler versions (output_head_sampler.rs:14-18; spec 06 sections 6-7) */
+#define YSKN_SMP_VERSION_INVERSE_CDF 2
+#define YSKN_SMP_VERSION_GUMBEL 3
+
+typedef struct yskn_smp* yskn_smp_handle;
+
+/* Per-row sampling parameters. Replaces the reference's Q35SmpParams
+ * (src/q35.hpp:114-116) set through yskn_set_opt keys 10/11/12/13/16/29
+ * (src/engine35.cpp:946-959) and yskn-ref SamplingParameters
+ * (output_head_sampler.rs:21-41). Stored values are binary64
+ * thousandths / 1000.0 (division, output_head_sampler.rs:46-49). */
+typedef struct yskn_smp_params {
+  uint32_t temperature_milli; /* 0 = greedy (real_engine.rs:241-243); else T = value / 1000.0 */
+  uint32_t top_p_milli;       /* 1..1000 */
+  uint32_t top_k;             /* 1..min(20, V); with EXTENDED_TOP_K: 0 (disabled) or 1..V */
+  uint32_t min_p_milli;       /* 0..1000 */
+  uint64_t seed;              /* full 64-bit seed (the C setter supplies uint64(uint32(v))) */
+  int32_t version;            /* YSKN_SMP_VERSION_GUMBEL (default) or _INVERSE_CDF */
+  /* EXTENSION (no reference counterpart): penalties over the token history
+   * passed to yskn_smp_sample. For every token with count c > 0 in the row's
+   * history, in binary32 round-to-nearest:
+   *   if repetition != 1: l = l > 0 ? l / repetition : l * repetition
+   *   l = l - frequency * (float)c;  l = l - presence
+   * applied to the (widened) logit before every other stage. */
+  float repetition_penalty; /* 1 = off; must be > 0 */
+  float presence_penalty;   /* 0 = off */
+  float frequency_penalty;  /* 0 = off */
+} yskn_smp_params;
+
+/* Optional outputs and inputs of yskn_smp_sample. Every pointer is a device
+ * pointer or NULL. Replaces the optional outputs of Q35SmpArgs
+ * (top_val/top_idx [rows*8], topk_val/topk_idx [rows*20]; src/q35.hpp:117-120)
+ * and the argmax of ArgmaxArgs (src/args.hpp:24-30). */
+typedef struct yskn_smp_aux {
+  uint32_t* argmax;      /* [rows] greedy id: larger logit, then smaller id */
+  uint32_t* top8_ids;    /* [rows*8] highest raw logits, (value desc, id asc) */
+  float* top8_vals;      /* [rows*8] */
+  uint32_t* top20_ids;   /* [rows*20] */
+  float* top20_vals;     /* [rows*20] */
+  /* EXTENSION: the n_logprobs highest raw logits with their logprobs
+   * l - max - log(sum_v exp(l_v - max)) in binary64 (the negated
+   * negative_log_likelihood of output_head_sampler.rs:230-250). */
+  int32_t n_logprobs;    /* 0..64 */
+  uint32_t* logprob_ids; /* [rows*n_logprobs] */
+  double* logprobs;      /* [rows*n_logprobs] */
+  int32_t* row_status;   /* [rows] per-row YSKN_SMP_* status */
+  /* EXTENSION: token history for the penalties (row r uses
+   * history[r*history_ld .. + history_len[r]]). */
+  const uint32_t* history;
+  const int32_t* history_len; /* [rows] */
+  int64_t history_ld;
+} yskn_smp_aux;
+
+/* Result of a speculative verification; mirrors the accept loop of
+ * crates/yskn-ref/src/speculation.rs:483-523 and src/specx.cpp:376-440. */
+typedef struct yskn_smp_verify_result {
+  uint32_t accepted; /* drafts equal to the selected token among emitted rows */
+  uint32_t emitted;  /* tokens produced: accepted drafts + correction or bonus */
+  uint32_t token;    /* last emitted token: the correction, or the bonus token */
+  int32_t stop_eos;  /* 1 if an EOS id ended the pass */
+} yskn_smp_verify_result;
+
+/* Thread-local description of the last failure on this thread
+ * (src/c_api.cpp:11-14 yskn_last_error). Never NULL. */
+const char* yskn_smp_last_error(void);
+
+/* Create a sampler for up to max_rows rows of up to max_vocab logits. The
+ * handle owns only scratch memory (candidates, counters, sort buffers),
+ * allocated once here like the engine's buffers (src/engine35.cpp:336-347).
+ * Initial parameters are the reference defaults (output_head_sampler.rs:30-41:
+ * T 1.0, top-p 0.95, top-k 20, min-p 0, seed 0, Gumbel). */
+int yskn_smp_create(int32_t max_rows, int32_t max_vocab, uint32_t flags, yskn_smp_handle* out);
+void yskn_smp_destroy(yskn_smp_handle h);
+
+/* Set sampling parameters: n = 1 applies one set to every row (the
+ * reference's single Q35SmpParams per launch); n = rows gives each row its own
+ * set (EXTENSION). Validates like SamplingParameters::validate
+ * (output_head_sampler.rs:56-75) against max_vocab; the top_k <= V check is
+ * repeated at every call against the call's V. Synchronous, like
+ * yskn_set_opt's cudaMemcpy (src/engine35.cpp:946-959). */
+int yskn_smp_set_params(yskn_smp_handle h, const yskn_smp_params* params, int32_t n);
+
+/* Sample one token per (row, draw). Replaces launch_q35_smp
+ * (src/q35.hpp:113-122; src/q35_sample.cu:210-214) and yskn-ref
+ * Sampler::sample (output_head_sampler.rs:86-92). Rows whose temperature is 0
+ * are greedy.
+ *   logits     device [rows x ld] elements of dtype (YSKN_SMP_F32 | _BF16)
+ *   positions  device [rows x n_draws] absolute prediction positions
+ *              (input position + 1; speculation.rs:490-492, spec 06 section 5)
+ *   out_ids    device [rows x n_draws]
+ *   aux        optional outputs/inputs (may be NULL)
+ * n_draws > 1 draws several positions from the same row (one candidate
+ * extraction). Asynchronous on `stream`; per-row errors land in
+ * aux->row_status and in the handle (see yskn_smp_sync). */
+int yskn_smp_sample(yskn_smp_handle h, const void* logits, int32_t dtype, int32_t rows,
+                    int32_t vocab, int64_t ld, const uint64_t* positions, int32_t n_draws,
+                    uint32_t* out_ids, const yskn_smp_aux* aux, void* stream);
+
+/* Greedy argmax per row: greedy() (output_head_sampler.rs:103-113),
+ * launch_argmax (src/args.hpp:24-30; src/misc_kernels.cu:57-96). */
+int yskn_smp_argmax(yskn_smp_handle h, const void* logits, int32_t dtype, int32_t rows,
+                    int32_t vocab, int64_t ld, uint32_t* out_ids, void* stream);
+
+/* The `count` (<= 64) highest raw logits per row in (value desc, id asc)
+ * order: top_tokens() (output_head_sampler.rs:115-134), launch_topk8
+ * (src/args.hpp:43-45; src/misc_kernels.cu:100-147). */
+int yskn_smp_top_tokens(yskn_smp_handle h, const void* logits, int32_t dtype, int32_t rows,
+                        int32_t vocab, int64_t ld, int32_t count, uint32_t* out_ids,
+                        float* out_vals, void* stream);
+
+/* Negative log-likelihood of targets[row]: negative_log_likelihood()
+ * (output_head_sampler.rs:230-250), launch_nll (src/misc_kernels.cu:150-166).
+ * Binary64 output. */
+int yskn_smp_nll(yskn_smp_handle h, const void* logits, int32_t dtype, int32_t rows,
+                 int32_t vocab, int64_t ld, const uint32_t* targets, double* out_nll,
+                 void* stream);
+
+/* One-launch speculative verification of M rows: row j is sampled at
+ * prediction position *base_position + j + 1 with the row-0 parameters,
+ * drafts[j] (j < M-1) is accepted while it equals the selected token, and the
+ * first mismatch's selection (or the bonus when all match) ends the pass; an
+ * EOS id among the emitted tokens stops it. Replaces the per-row Selector loop
+ * of speculation.rs:483-523 and the host accept loop of src/specx.cpp:376-440.
+ *   target_logits device [M x ld]; drafts device [M-1]; base_position device [1]
+ *   eos_ids device [n_eos] (may be NULL when n_eos = 0)
+ *   out_ids device [M] selected token per row; result device [1] */
+int yskn_smp_verify(yskn_smp_handle h, const void* target_logits, int32_t dtype, int32_t M,
+                    int32_t vocab, int64_t ld, const uint32_t* drafts,
+                    const uint64_t* base_position, const uint32_t* eos_ids, int32_t n_eos,
+                    uint32_t* out_ids, yskn_smp_verify_result* result, void* stream);
+
+/* Synchronise `stream` and return the first per-row error of the handle's
+ * last call (YSKN_SMP_OK if none), setting yskn_smp_last_error(). */
+int yskn_smp_sync(yskn_smp_handle h, void* stream);
+
+/* Host-slice convenience with the exact signature semantics of the Rust
+ * trait Selector::select(&mut self, logits: &[f32], prediction_position: u64)
+ * (crates/yskn-ref/src/speculation.rs:121-131): copies `vocab` host logits to
+ * the device, samples with row-0 parameters, returns the token synchronously. */
+int yskn_smp_select_host(yskn_smp_handle h, const float* host_logits, int32_t vocab,
+                         uint64_t prediction_position, uint32_t* out_token);
+
+/* Validate parameters on the host without a device (the reference's
+ * SamplingParameters::validate, output_head_sampler.rs:56-75). */
+int yskn_smp_validate_params(const yskn_smp_params* params, int32_t vocab, uint32_t flags);
+
+/* Library version string. */
+const char* yskn_smp_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* YSKN_SMP_H */

@@ -1,0 +1,346 @@
+"""Parity of the HIP sampler (through the C ABI) with the CPU oracle.
+
+Bit-exact: sampled token ids, argmax, top-8 / top-20 / top-N id lists and
+values, verification counts. Logprobs and NLL: 1e-5 relative (absolute floor
+1e-10). Inputs are seeded and identical for both sides.
+"""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+import yskn_oracle as O
+from gpu_helpers import assert_logprobs_close, oracle_params, oracle_select, pmap, to_u32
+
+pytestmark = pytest.mark.gpu
+
+from yskn_smp import (GUMBEL, INVERSE_CUMULATIVE, DeviceSampler, InvalidInput, NonFinite,
+                      SamplingParameters)
+from yskn_smp import synth
+
+DEV = "cuda"
+
+
+def _run(dev, x, positions, **kw):
+    out = dev.sample(x, torch.as_tensor(positions, dtype=torch.int64, device=DEV), **kw)
+    dev.sync()
+    return out
+
+
+@pytest.fixture(scope="module")
+def small_dev():
+    d = DeviceSampler(64, 70_000, extended_top_k=True)
+    yield d
+    d.close()
+
+
+# ---------------------------------------------------------------------------
+# edge cases on small rows
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize("V", [1, 2, 3, 5, 8, 17, 64, 1000, 16383, 16384, 16385, 40000, 65537])
+def test_small_rows_all_outputs(small_dev, V):
+    rng = np.random.default_rng(V)
+    rows = 6
+    x = (2.0 * rng.standard_normal((rows, V))).astype(np.float32)
+    x[1] = np.round(x[1])                      # heavy ties
+    x[2, : V // 2] = -0.0                      # signed zeros
+    x[2, V // 2:] = 0.0
+    xt = torch.from_numpy(x).to(DEV)
+    k = min(20, V)
+    for version in (GUMBEL, INVERSE_CUMULATIVE):
+        sp = SamplingParameters(temperature_milli=900, top_p_milli=950, top_k=k, seed=99 + V,
+                                version=version)
+        small_dev.set_params(sp)
+        pos = rng.integers(0, 2 ** 40, rows)
+        out = _run(small_dev, xt, pos, argmax=True, top8=V >= 8, top20=V >= 20)
+        ids = to_u32(out["ids"]).reshape(-1)
+        ref = pmap(lambda r: oracle_select(x[r], int(pos[r]), sp), range(rows))
+        assert list(ids) == ref
+        am = to_u32(out["argmax"])
+        assert list(am) == [O.greedy(x[r]) for r in range(rows)]
+        for n in (8, 20):
+            if V >= n:
+                got = to_u32(out[f"top{n}_ids"])
+                vals = out[f"top{n}_vals"].cpu().numpy()
+                for r in range(rows):
+                    tt = O.top_tokens(x[r], n)
+                    assert list(got[r]) == list(tt)
+                    assert np.array_equal(vals[r].view(np.uint32), x[r][tt].view(np.uint32))
+
+
+def test_all_equal_row_uses_smallest_ids(small_dev):
+    V = 50_000
+    x = torch.full((2, V), 0.25, dtype=torch.float32, device=DEV)
+    sp = SamplingParameters(top_k=20, seed=3)
+    small_dev.set_params(sp)
+    out = _run(small_dev, x, [5, 6], argmax=True, top20=True)
+    assert list(to_u32(out["argmax"])) == [0, 0]
+    assert list(to_u32(out["top20_ids"])[0]) == list(range(20))
+    xn = x.cpu().numpy()
+    assert list(to_u32(out["ids"]).reshape(-1)) == [oracle_select(xn[0], 5, sp),
+                                                    oracle_select(xn[1], 6, sp)]
+
+
+@pytest.mark.parametrize("bad", [math.nan, math.inf, -math.inf])
+def test_nonfinite_rows_are_rejected(small_dev, bad):
+    x = torch.zeros((3, 1000), dtype=torch.float32, device=DEV)
+    x[1, 500] = bad
+    small_dev.set_params(SamplingParameters())
+    out = small_dev.sample(x, torch.tensor([1, 2, 3], device=DEV), row_status=True)
+    with pytest.raises(NonFinite):
+        small_dev.sync()
+    st = out["status"].cpu().tolist()
+    assert st == [0, -2, 0]
+    assert to_u32(out["ids"])[1, 0] == 0xFFFFFFFF
+
+
+def test_parameter_validation_mirrors_reference():
+    d = DeviceSampler(1, 100)
+    for kw in [dict(top_k=0), dict(top_k=21), dict(top_p_milli=0), dict(top_p_milli=1001),
+               dict(min_p_milli=1001), dict(version=4)]:
+        with pytest.raises(InvalidInput):
+            d.set_params(SamplingParameters(**kw))
+    x = torch.zeros((1, 10), dtype=torch.float32, device=DEV)
+    d.set_params(SamplingParameters(top_k=20))
+    with pytest.raises(InvalidInput):      # top_k > V
+        d.sample(x, torch.tensor([0], device=DEV))
+    with pytest.raises(InvalidInput):      # V over the handle's limit
+        d.sample(torch.zeros((1, 101), device=DEV), torch.tensor([0], device=DEV))
+    d.close()
+
+
+def test_misaligned_rows_use_the_scalar_path(small_dev):
+    rng = np.random.default_rng(77)
+    V, ld = 33_333, 33_335
+    base = torch.from_numpy((1.5 * rng.standard_normal(4 * ld + 1)).astype(np.float32)).to(DEV)
+    x = base[1:1 + 4 * ld].view(4, ld)[:, :V]     # odd offset and stride
+    sp = SamplingParameters(top_k=20, seed=5)
+    small_dev.set_params(sp)
+    out = _run(small_dev, x, [1, 2, 3, 4], top20=True)
+    xn = x.cpu().numpy()
+    assert list(to_u32(out["ids"]).reshape(-1)) == [oracle_select(xn[r], r + 1, sp) for r in range(4)]
+    for r in range(4):
+        assert list(to_u32(out["top20_ids"])[r]) == list(O.top_tokens(xn[r], 20))
+
+
+def test_many_draws_from_one_row(small_dev):
+    rng = np.random.default_rng(1)
+    x = (2.5 * rng.standard_normal((1, 30_000))).astype(np.float32)
+    sp = SamplingParameters(top_k=20, seed=11)
+    small_dev.set_params(sp)
+    pos = np.arange(300, 812)
+    out = _run(small_dev, torch.from_numpy(x).to(DEV), pos.reshape(1, -1))
+    ref = O.sample_positions(x[0], pos.astype(np.uint64), oracle_params(sp))
+    assert np.array_equal(to_u32(out["ids"]).reshape(-1), ref)
+
+
+@pytest.mark.parametrize("T,tp,mp,k", [(1, 1000, 0, 20), (5000, 1000, 0, 20), (300, 500, 100, 7),
+                                       (1000, 1000, 1000, 20), (2000, 10, 0, 20)])
+def test_parameter_corners(small_dev, T, tp, mp, k):
+    rng = np.random.default_rng(T + tp)
+    x = (3.0 * rng.standard_normal((8, 20_000))).astype(np.float32)
+    for version in (GUMBEL, INVERSE_CUMULATIVE):
+        sp = SamplingParameters(temperature_milli=T, top_p_milli=tp, min_p_milli=mp, top_k=k,
+                                seed=1234, version=version)
+        small_dev.set_params(sp)
+        pos = np.arange(8) * 1000 + 7
+        out = _run(small_dev, torch.from_numpy(x).to(DEV), pos)
+        assert list(to_u32(out["ids"]).reshape(-1)) == [oracle_select(x[r], int(pos[r]), sp)
+                                                        for r in range(8)]
+
+
+@pytest.mark.parametrize("k", [0, 21, 64, 65, 500, 20_000])
+def test_extended_top_k(small_dev, k):
+    rng = np.random.default_rng(k + 1)
+    x = (rng.standard_normal((6, 20_000)) * np.array([[0.5], [1], [2], [4], [8], [30]])).astype(np.float32)
+    for version in (GUMBEL, INVERSE_CUMULATIVE):
+        sp = SamplingParameters(temperature_milli=800, top_p_milli=930, min_p_milli=0, top_k=k,
+                                seed=77, version=version)
+        small_dev.set_params(sp)
+        pos = np.arange(6) + 50
+        out = _run(small_dev, torch.from_numpy(x).to(DEV), pos)
+        ref = pmap(lambda r: oracle_select(x[r], int(pos[r]), sp, extension=True), range(6))
+        assert list(to_u32(out["ids"]).reshape(-1)) == ref
+
+
+def test_per_row_parameters_and_greedy_rows(small_dev):
+    rng = np.random.default_rng(9)
+    rows = 12
+    x = (2.0 * rng.standard_normal((rows, 25_000))).astype(np.float32)
+    sps = [SamplingParameters(temperature_milli=(0 if r % 4 == 0 else 300 + 100 * r),
+                              top_p_milli=800 + 15 * r, top_k=[1, 20, 50, 0][r % 4],
+                              min_p_milli=5 * r, seed=1000 + r,
+                              version=GUMBEL if r % 2 else INVERSE_CUMULATIVE) for r in range(rows)]
+    small_dev.set_params(sps)
+    pos = rng.integers(0, 10 ** 9, rows)
+    out = _run(small_dev, torch.from_numpy(x).to(DEV), pos)
+    ref = pmap(lambda r: oracle_select(x[r], int(pos[r]), sps[r], extension=True), range(rows))
+    assert list(to_u32(out["ids"]).reshape(-1)) == ref
+
+
+def test_bf16_rows(small_dev):
+    rng = np.random.default_rng(10)
+    x = torch.from_numpy((2 * rng.standard_normal((5, 30_001))).astype(np.float32)).to(torch.bfloat16)
+    sp = SamplingParameters(temperature_milli=700, top_p_milli=900, min_p_milli=50, seed=4)
+    small_dev.set_params(sp)
+    out = _run(small_dev, x.to(DEV), [1, 2, 3, 4, 5], top20=True)
+    xf = x.float().numpy()
+    assert list(to_u32(out["ids"]).reshape(-1)) == [oracle_select(xf[r], r + 1, sp) for r in range(5)]
+    for r in range(5):
+        assert list(to_u32(out["top20_ids"])[r]) == list(O.top_tokens(xf[r], 20))
+
+
+def test_penalties_small(small_dev):
+    rng = np.random.default_rng(12)
+    V = 5000
+    x = (2 * rng.standard_normal((3, V))).astype(np.float32)
+    hist = rng.integers(0, 200, (3, 700)).astype(np.int32)   # concentrated history
+    hl = np.array([700, 0, 333], np.int32)
+    sp = SamplingParameters(temperature_milli=700, top_p_milli=900, min_p_milli=50, seed=8,
+                            repetition_penalty=1.05, presence_penalty=0.5, frequency_penalty=0.3)
+    small_dev.set_params(sp)
+    out = _run(small_dev, torch.from_numpy(x).to(DEV), [10, 11, 12], top20=True,
+               history=torch.from_numpy(hist).to(DEV), history_len=torch.from_numpy(hl).to(DEV))
+    for r in range(3):
+        y = O.apply_penalties(x[r], hist[r, :hl[r]], 1.05, 0.5, 0.3)
+        assert to_u32(out["ids"])[r, 0] == oracle_select(y, 10 + r, sp)
+        tt = O.top_tokens(y, 20)
+        assert list(to_u32(out["top20_ids"])[r]) == list(tt)
+        assert np.array_equal(out["top20_vals"][r].cpu().numpy().view(np.uint32), y[tt].view(np.uint32))
+
+
+def test_top_tokens_and_nll_apis(small_dev):
+    rng = np.random.default_rng(13)
+    x = (3 * rng.standard_normal((7, 12_345))).astype(np.float32)
+    xt = torch.from_numpy(x).to(DEV)
+    for count in (1, 8, 33, 64):
+        ids, vals = small_dev.top_tokens(xt, count)
+        small_dev.sync()
+        for r in range(7):
+            assert list(to_u32(ids)[r]) == list(O.top_tokens(x[r], count))
+    tg = rng.integers(0, 12_345, 7)
+    nll = small_dev.nll(xt, torch.from_numpy(tg).to(DEV))
+    small_dev.sync()
+    assert_logprobs_close(nll.cpu().numpy(), [O.nll(x[r], int(tg[r])) for r in range(7)])
+
+
+def test_dense_path_matches_compact_path():
+    rng = np.random.default_rng(14)
+    V = 40_000
+    x = (rng.standard_normal((6, V)) * np.array([[0.3], [1], [2], [5], [20], [100]])).astype(np.float32)
+    xt = torch.from_numpy(x).to(DEV)
+    a = DeviceSampler(6, V, extended_top_k=True)
+    b = DeviceSampler(6, V, extended_top_k=True, force_dense=True)
+    for k in (20, 0):
+        sp = SamplingParameters(temperature_milli=1000, top_p_milli=950, top_k=k, seed=21)
+        a.set_params(sp)
+        b.set_params(sp)
+        pos = np.arange(6) + 3
+        oa = _run(a, xt, pos, argmax=True, top20=True, n_logprobs=20)
+        ob = _run(b, xt, pos, argmax=True, top20=True, n_logprobs=20)
+        for key in ("ids", "argmax", "top20_ids", "logprob_ids"):
+            assert torch.equal(oa[key], ob[key]), key
+        ref = pmap(lambda r: oracle_select(x[r], int(pos[r]), sp, extension=True), range(6))
+        assert list(to_u32(ob["ids"]).reshape(-1)) == ref
+    a.close()
+    b.close()
+
+
+# ---------------------------------------------------------------------------
+# the five workloads at full size
+# ---------------------------------------------------------------------------
+def test_single_row_1024_draws():
+    x = synth.single_row(DEV)
+    d = DeviceSampler(1, synth.V_SMALL)
+    sp = SamplingParameters(temperature_milli=1000, top_p_milli=950, top_k=20, min_p_milli=0, seed=0)
+    d.set_params(sp)
+    pos = np.arange(1024)
+    out = _run(d, x, pos.reshape(1, -1), argmax=True, top20=True)
+    xn = x.cpu().numpy()[0]
+    assert to_u32(out["argmax"])[0] == O.greedy(xn)
+    ref = O.sample_positions(xn, pos.astype(np.uint64), oracle_params(sp))
+    assert np.array_equal(to_u32(out["ids"]).reshape(-1), ref)
+    assert list(to_u32(out["top20_ids"])[0]) == list(O.top_tokens(xn, 20))
+    d.close()
+
+
+@pytest.mark.parametrize("M", [8, 9])
+def test_spec_verify(M):
+    tgt, drf = synth.spec_verify(M, DEV)
+    sp = SamplingParameters(temperature_milli=1000, top_p_milli=950, top_k=20, seed=0x5EC)
+    base = 10_000
+    drn, tgn = drf.cpu().numpy(), tgt.cpu().numpy()
+    drafts = [oracle_select(drn[j], base + j + 1, sp) for j in range(M - 1)]
+    d = DeviceSampler(M, synth.V_LARGE)
+    d.set_params(sp)
+    ids, res, _keep = d.verify(tgt, torch.tensor(drafts, device=DEV), torch.tensor([base], device=DEV))
+    d.sync()
+    sel, em, acc, stop = O.verify(tgn, drafts, base, oracle_params(sp))
+    r = res.cpu().numpy().astype(np.int64)
+    assert (r[0], r[1], r[3]) == (acc, em, int(stop))
+    assert r[2] == sel[-1]
+    assert list(to_u32(ids)[:em]) == list(sel)
+    # a wrong draft at depth 2 stops acceptance there
+    bad = list(drafts)
+    bad[2] = (bad[2] + 1) % synth.V_LARGE
+    ids, res, _keep = d.verify(tgt, torch.tensor(bad, device=DEV), torch.tensor([base], device=DEV))
+    d.sync()
+    sel, em, acc, stop = O.verify(tgn, bad, base, oracle_params(sp))
+    r = res.cpu().numpy().astype(np.int64)
+    assert (r[0], r[1], r[2]) == (acc, em, sel[-1])
+    d.close()
+
+
+def test_penalties_workload():
+    x, hist = synth.penalties(DEV)
+    sp = SamplingParameters(temperature_milli=700, top_p_milli=900, min_p_milli=50, top_k=20,
+                            seed=31, repetition_penalty=1.05, presence_penalty=0.5,
+                            frequency_penalty=0.3)
+    d = DeviceSampler(1, synth.V_LARGE)
+    d.set_params(sp)
+    pos = np.arange(1)
+    out = _run(d, x, pos, top20=True, history=hist.reshape(1, -1))
+    xf = x.float().cpu().numpy()[0]
+    y = O.apply_penalties(xf, hist.cpu().numpy(), 1.05, 0.5, 0.3)
+    assert to_u32(out["ids"])[0, 0] == oracle_select(y, 0, sp)
+    assert list(to_u32(out["top20_ids"])[0]) == list(O.top_tokens(y, 20))
+    d.close()
+
+
+def test_batched_heterogeneous():
+    x = synth.batched(64, DEV)
+    pr = synth.batched_params(64)
+    sps = [SamplingParameters(temperature_milli=p["temperature_milli"], top_p_milli=p["top_p_milli"],
+                              min_p_milli=p["min_p_milli"], top_k=p["top_k"], seed=p["seed"])
+           for p in pr]
+    pos = np.array([p["position"] for p in pr])
+    d = DeviceSampler(64, synth.V_LARGE, extended_top_k=True)
+    d.set_params(sps)
+    out = _run(d, x, pos, argmax=True)
+    xn = x.cpu().numpy()
+    ref = pmap(lambda r: oracle_select(xn[r], int(pos[r]), sps[r], extension=True), range(64))
+    assert list(to_u32(out["ids"]).reshape(-1)) == ref
+    assert list(to_u32(out["argmax"])) == [int(np.argmax(xn[r])) for r in range(64)]
+    d.close()
+
+
+def test_large_batch_top_p_with_logprobs():
+    rows = 256
+    x = synth.large_batch(rows, DEV)
+    seeds = synth.large_batch_seeds(rows)
+    sps = [SamplingParameters(temperature_milli=1000, top_p_milli=950, top_k=0, seed=s) for s in seeds]
+    d = DeviceSampler(rows, synth.V_LARGE, extended_top_k=True)
+    d.set_params(sps)
+    pos = np.arange(rows) + 1
+    out = _run(d, x, pos, n_logprobs=20)
+    xn = x.cpu().numpy()
+    ref = pmap(lambda r: oracle_select(xn[r], int(pos[r]), sps[r], extension=True), range(rows))
+    assert list(to_u32(out["ids"]).reshape(-1)) == ref
+    lps = pmap(lambda r: O.top_logprobs(xn[r], 20), range(rows))
+    got_ids = to_u32(out["logprob_ids"])
+    got_lp = out["logprobs"].cpu().numpy()
+    for r in range(rows):
+        assert list(got_ids[r]) == list(lps[r][0])
+        assert_logprobs_close(got_lp[r], lps[r][1])
+    d.close()

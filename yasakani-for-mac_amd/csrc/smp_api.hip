@@ -1,0 +1,497 @@
+// smp_api.hip -- host side of the C ABI declared in include/yskn_smp.h.
+//
+// Validation mirrors the reference: SamplingParameters::validate
+// (crates/yskn-ref/src/output_head_sampler.rs:56-75), validate_logits
+// (:94-101), and the C ABI's 0 / negative status with a thread-local last
+// error (src/c_api.cpp:11-14). The handle owns only scratch memory,
+// allocated once at create (the engine's pattern, src/engine35.cpp:336-347).
+#include <hip/hip_runtime.h>
+
+#include <cstdio>
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "../../include/yskn_smp.h"
+#include "smp_internal.hpp"
+
+using namespace yskn;
+
+namespace {
+
+thread_local std::string g_error;
+
+int fail(int code, const std::string& msg) {
+  g_error = msg;
+  return code;
+}
+
+int hip_fail(hipError_t e, const char* what) {
+  g_error = std::string(what) + ": " + hipGetErrorString(e);
+  return YSKN_SMP_EDEVICE;
+}
+
+constexpr int SPIN_LIMIT = 4096;
+
+}  // namespace
+
+struct yskn_smp {
+  int32_t max_rows = 0;
+  int32_t max_vocab = 0;
+  uint32_t flags = 0;
+  int32_t max_segments = 0;
+  int device = 0;
+  std::vector<yskn_smp_params> params;  // host copy, 1 or max_rows entries
+  bool params_shared = true;
+  DevParams* d_params = nullptr;
+  uint64_t* d_seg_cand = nullptr;
+  SegInfo* d_seg_info = nullptr;
+  RowSync* d_sync = nullptr;
+  int32_t* d_status = nullptr;
+  uint32_t* d_vcount = nullptr;
+  uint32_t* d_vresult = nullptr;
+  uint64_t* d_dense_a = nullptr;
+  uint64_t* d_dense_b = nullptr;
+  double* d_dense_w = nullptr;
+  int64_t dense_ld = 0;
+  uint32_t* d_pen_bitmap = nullptr;
+  int64_t bm_ld = 0;
+  uint32_t* d_pen_ids = nullptr;
+  uint32_t* d_pen_cnt = nullptr;
+  int32_t* d_pen_len = nullptr;
+  unsigned long long* d_stats = nullptr;
+  // host-slice convenience buffers
+  float* d_host_logits = nullptr;
+  uint64_t* d_host_pos = nullptr;
+  uint32_t* d_host_out = nullptr;
+  int32_t last_rows = 0;
+};
+
+namespace {
+
+yskn_smp_params default_params() {
+  yskn_smp_params p;
+  std::memset(&p, 0, sizeof p);
+  p.temperature_milli = 1000;
+  p.top_p_milli = 950;
+  p.top_k = 20;
+  p.min_p_milli = 0;
+  p.seed = 0;
+  p.version = YSKN_SMP_VERSION_GUMBEL;
+  p.repetition_penalty = 1.0f;
+  p.presence_penalty = 0.0f;
+  p.frequency_penalty = 0.0f;
+  return p;
+}
+
+bool finite_f(float x) {
+  uint32_t b;
+  std::memcpy(&b, &x, 4);
+  return (b & 0x7f800000u) != 0x7f800000u;
+}
+
+int validate(const yskn_smp_params& p, int64_t vocab, uint32_t flags) {
+  if (p.temperature_milli != 0) {
+    // T = temperature_milli / 1000.0 is finite and positive by construction.
+    if (p.top_p_milli < 1 || p.top_p_milli > 1000)
+      return fail(YSKN_SMP_EINVAL, "invalid input: top_p must be in (0, 1]");
+    if (p.min_p_milli > 1000) return fail(YSKN_SMP_EINVAL, "invalid input: min_p must be in [0, 1]");
+    if (flags & YSKN_SMP_FLAG_EXTENDED_TOP_K) {
+      if ((int64_t)p.top_k > vocab)
+        return fail(YSKN_SMP_EINVAL, "invalid input: top_k must be in 0..=vocabulary size");
+    } else if (p.top_k == 0 || p.top_k > 20 || (int64_t)p.top_k > vocab) {
+      return fail(YSKN_SMP_EINVAL, "invalid input: top_k must be in 1..=min(20, vocabulary size)");
+    }
+    if (p.version != YSKN_SMP_VERSION_GUMBEL && p.version != YSKN_SMP_VERSION_INVERSE_CDF)
+      return fail(YSKN_SMP_EINVAL, "invalid input: version must be 2 or 3");
+  }
+  if (!finite_f(p.repetition_penalty) || !(p.repetition_penalty > 0.0f) ||
+      !finite_f(p.presence_penalty) || !finite_f(p.frequency_penalty))
+    return fail(YSKN_SMP_EINVAL, "invalid input: penalties must be finite, repetition > 0");
+  return YSKN_SMP_OK;
+}
+
+DevParams to_device(const yskn_smp_params& p) {
+  DevParams d;
+  std::memset(&d, 0, sizeof d);
+  // binary64 division by 1000.0, not multiplication by 0.001
+  d.temperature = (double)p.temperature_milli / 1000.0;
+  d.top_p = (double)p.top_p_milli / 1000.0;
+  d.min_p = (double)p.min_p_milli / 1000.0;
+  d.seed = p.seed;
+  d.top_k = p.top_k;
+  d.version = p.version;
+  d.greedy = p.temperature_milli == 0 ? 1 : 0;
+  d.rep = p.repetition_penalty;
+  d.pres = p.presence_penalty;
+  d.freq = p.frequency_penalty;
+  d.penalize = (p.repetition_penalty != 1.0f || p.presence_penalty != 0.0f ||
+                p.frequency_penalty != 0.0f)
+                   ? 1
+                   : 0;
+  return d;
+}
+
+template <typename T>
+hipError_t alloc(T** p, size_t n) {
+  return hipMalloc((void**)p, n * sizeof(T) + 256);
+}
+
+int check_common(yskn_smp_handle h, const void* logits, int32_t dtype, int32_t rows,
+                 int32_t vocab, int64_t ld) {
+  if (!h) return fail(YSKN_SMP_EINVAL, "invalid input: null handle");
+  if (!logits) return fail(YSKN_SMP_EINVAL, "invalid input: null logits");
+  if (dtype != YSKN_SMP_F32 && dtype != YSKN_SMP_BF16)
+    return fail(YSKN_SMP_EINVAL, "invalid input: dtype must be YSKN_SMP_F32 or YSKN_SMP_BF16");
+  if (vocab <= 0)
+    return fail(YSKN_SMP_EINVAL, "invalid input: logits must contain a nonempty u32-indexed vocabulary");
+  if (vocab > h->max_vocab)
+    return fail(YSKN_SMP_ERANGE, "vocabulary larger than the handle's max_vocab");
+  if (rows <= 0 || rows > h->max_rows) return fail(YSKN_SMP_ERANGE, "rows outside 1..=max_rows");
+  if (ld < vocab) return fail(YSKN_SMP_EINVAL, "invalid input: ld < vocab");
+  return YSKN_SMP_OK;
+}
+
+int check_params_for(yskn_smp_handle h, int32_t rows, int32_t vocab) {
+  const int n = h->params_shared ? 1 : rows;
+  for (int r = 0; r < n; ++r) {
+    const int st = validate(h->params[r], vocab, h->flags);
+    if (st) return st;
+  }
+  return YSKN_SMP_OK;
+}
+
+bool any_penalty(yskn_smp_handle h, int32_t rows) {
+  const int n = h->params_shared ? 1 : rows;
+  for (int r = 0; r < n; ++r) {
+    const yskn_smp_params& p = h->params[r];
+    if (p.repetition_penalty != 1.0f || p.presence_penalty != 0.0f || p.frequency_penalty != 0.0f)
+      return true;
+  }
+  return false;
+}
+
+SmpArgs base_args(yskn_smp_handle h, const void* logits, int32_t rows, int32_t vocab,
+                  int64_t ld) {
+  SmpArgs a;
+  std::memset(&a, 0, sizeof a);
+  a.logits = logits;
+  a.ld = ld;
+  a.V = vocab;
+  a.rows = rows;
+  a.S = (vocab + SEG - 1) / SEG;
+  a.mode = MODE_SAMPLE;
+  a.prm = h->d_params;
+  a.prm_shared = h->params_shared ? 1 : 0;
+  a.n_draws = 1;
+  a.status = h->d_status;
+  a.pen_bitmap = h->d_pen_bitmap;
+  a.bm_ld = h->bm_ld;
+  a.pen_ids = h->d_pen_ids;
+  a.pen_cnt = h->d_pen_cnt;
+  a.pen_len = h->d_pen_len;
+  a.seg_cand = h->d_seg_cand;
+  a.seg_info = h->d_seg_info;
+  a.sync = h->d_sync;
+  a.dense_a = h->d_dense_a;
+  a.dense_b = h->d_dense_b;
+  a.dense_w = h->d_dense_w;
+  a.dense_ld = h->dense_ld;
+  a.force_dense = (h->flags & YSKN_SMP_FLAG_FORCE_DENSE) ? 1 : 0;
+  a.spin_limit = SPIN_LIMIT;
+  a.stats = h->d_stats;
+  return a;
+}
+
+bool vector_ok(const void* logits, int32_t dtype, int64_t ld) {
+  const size_t es = dtype == YSKN_SMP_F32 ? 4 : 2;
+  return ((uintptr_t)logits % 16 == 0) && ((ld * (int64_t)es) % 16 == 0);
+}
+
+int launch(yskn_smp_handle h, SmpArgs& a, int32_t dtype, bool pen, const yskn_smp_aux* aux,
+           hipStream_t st) {
+  if (pen) {
+    PenArgs p;
+    std::memset(&p, 0, sizeof p);
+    p.history = aux ? aux->history : nullptr;
+    p.history_len = aux ? aux->history_len : nullptr;
+    p.history_ld = aux ? aux->history_ld : 0;
+    p.V = a.V;
+    p.rows = a.rows;
+    p.bitmap = h->d_pen_bitmap;
+    p.bm_ld = h->bm_ld;
+    p.ids = h->d_pen_ids;
+    p.cnt = h->d_pen_cnt;
+    p.len = h->d_pen_len;
+    p.prm = h->d_params;
+    p.prm_shared = a.prm_shared;
+    hipError_t e = launch_penalty_prep(p, st);
+    if (e != hipSuccess) return hip_fail(e, "penalty preparation launch");
+  }
+  hipError_t e = launch_sample(a, dtype == YSKN_SMP_F32 ? 0 : 1, vector_ok(a.logits, dtype, a.ld),
+                               pen, st);
+  if (e != hipSuccess) return hip_fail(e, "sampler launch");
+  h->last_rows = a.rows;
+  return YSKN_SMP_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* yskn_smp_last_error(void) { return g_error.c_str(); }
+
+const char* yskn_smp_version(void) { return "yskn_smp 0.1 (gfx950)"; }
+
+int yskn_smp_validate_params(const yskn_smp_params* params, int32_t vocab, uint32_t flags) {
+  if (!params) return fail(YSKN_SMP_EINVAL, "invalid input: null params");
+  return validate(*params, vocab, flags);
+}
+
+int yskn_smp_create(int32_t max_rows, int32_t max_vocab, uint32_t flags, yskn_smp_handle* out) {
+  if (!out) return fail(YSKN_SMP_EINVAL, "invalid input: null output handle");
+  *out = nullptr;
+  if (max_rows <= 0) return fail(YSKN_SMP_EINVAL, "invalid input: max_rows must be positive");
+  if (max_vocab <= 0)
+    return fail(YSKN_SMP_EINVAL, "invalid input: logits must contain a nonempty u32-indexed vocabulary");
+  if ((int64_t)max_vocab > (int64_t)SEG * MAX_SEGMENTS)
+    return fail(YSKN_SMP_ERANGE, "vocabulary larger than 16,777,216");
+  yskn_smp* h = new yskn_smp();
+  h->max_rows = max_rows;
+  h->max_vocab = max_vocab;
+  h->flags = flags;
+  h->max_segments = (max_vocab + SEG - 1) / SEG;
+  h->params.assign(1, default_params());
+  h->params_shared = true;
+  if (hipGetDevice(&h->device) != hipSuccess) h->device = 0;
+  const size_t R = (size_t)max_rows, Sg = (size_t)h->max_segments;
+  h->dense_ld = ((int64_t)max_vocab + 63) / 64 * 64;
+  h->bm_ld = ((int64_t)max_vocab + 31) / 32;
+  hipError_t e = hipSuccess;
+  auto step = [&](hipError_t r) {
+    if (e == hipSuccess) e = r;
+  };
+  step(alloc(&h->d_params, R));
+  step(alloc(&h->d_seg_cand, R * Sg * CAPSEG));
+  step(alloc(&h->d_seg_info, R * Sg));
+  step(alloc(&h->d_sync, R));
+  step(alloc(&h->d_status, R));
+  step(alloc(&h->d_vcount, 4));
+  step(alloc(&h->d_vresult, 4));
+  step(alloc(&h->d_dense_a, R * (size_t)h->dense_ld));
+  step(alloc(&h->d_dense_b, R * (size_t)h->dense_ld));
+  step(alloc(&h->d_dense_w, R * (size_t)h->dense_ld));
+  step(alloc(&h->d_pen_bitmap, R * (size_t)h->bm_ld));
+  step(alloc(&h->d_pen_ids, R * (size_t)HCAP));
+  step(alloc(&h->d_pen_cnt, R * (size_t)HCAP));
+  step(alloc(&h->d_pen_len, R));
+  step(alloc(&h->d_stats, (size_t)STAT_COUNT));
+  step(alloc(&h->d_host_logits, (size_t)max_vocab));
+  step(alloc(&h->d_host_pos, 1));
+  step(alloc(&h->d_host_out, 1));
+  if (e == hipSuccess) step(hipMemset(h->d_sync, 0, R * sizeof(RowSync)));
+  if (e == hipSuccess) step(hipMemset(h->d_status, 0, R * sizeof(int32_t)));
+  if (e == hipSuccess) step(hipMemset(h->d_vcount, 0, 4 * sizeof(uint32_t)));
+  if (e == hipSuccess) step(hipMemset(h->d_pen_len, 0, R * sizeof(int32_t)));
+  if (e == hipSuccess) step(hipMemset(h->d_stats, 0, STAT_COUNT * sizeof(unsigned long long)));
+  if (e == hipSuccess) {
+    const DevParams d = to_device(h->params[0]);
+    step(hipMemcpy(h->d_params, &d, sizeof d, hipMemcpyHostToDevice));
+  }
+  if (e != hipSuccess) {
+    yskn_smp_destroy(h);
+    return hip_fail(e, "yskn_smp_create");
+  }
+  *out = h;
+  return YSKN_SMP_OK;
+}
+
+void yskn_smp_destroy(yskn_smp_handle h) {
+  if (!h) return;
+  void* ptrs[] = {h->d_params,     h->d_seg_cand,  h->d_seg_info,    h->d_sync,
+                  h->d_status,     h->d_vcount,    h->d_vresult,     h->d_dense_a,
+                  h->d_dense_b,    h->d_dense_w,   h->d_pen_bitmap,  h->d_pen_ids,
+                  h->d_pen_cnt,    h->d_pen_len,   h->d_stats,       h->d_host_logits,
+                  h->d_host_pos,   h->d_host_out};
+  for (void* p : ptrs)
+    if (p) (void)hipFree(p);
+  delete h;
+}
+
+int yskn_smp_set_params(yskn_smp_handle h, const yskn_smp_params* params, int32_t n) {
+  if (!h || !params) return fail(YSKN_SMP_EINVAL, "invalid input: null handle or params");
+  if (n != 1 && (n < 1 || n > h->max_rows))
+    return fail(YSKN_SMP_EINVAL, "invalid input: n must be 1 or 1..=max_rows");
+  for (int i = 0; i < n; ++i) {
+    const int st = validate(params[i], h->max_vocab, h->flags);
+    if (st) return st;
+  }
+  std::vector<DevParams> d(n);
+  for (int i = 0; i < n; ++i) d[i] = to_device(params[i]);
+  // Like the reference setter: drain outstanding work, then copy.
+  hipError_t e = hipDeviceSynchronize();
+  if (e == hipSuccess) e = hipMemcpy(h->d_params, d.data(), n * sizeof(DevParams), hipMemcpyHostToDevice);
+  if (e != hipSuccess) return hip_fail(e, "yskn_smp_set_params");
+  h->params.assign(params, params + n);
+  h->params_shared = n == 1;
+  return YSKN_SMP_OK;
+}
+
+int yskn_smp_sample(yskn_smp_handle h, const void* logits, int32_t dtype, int32_t rows,
+                    int32_t vocab, int64_t ld, const uint64_t* positions, int32_t n_draws,
+                    uint32_t* out_ids, const yskn_smp_aux* aux, void* stream) {
+  int st = check_common(h, logits, dtype, rows, vocab, ld);
+  if (st) return st;
+  if (!h->params_shared && rows > (int32_t)h->params.size())
+    return fail(YSKN_SMP_EINVAL, "invalid input: fewer per-row parameter sets than rows");
+  if (out_ids && (!positions || n_draws < 1))
+    return fail(YSKN_SMP_EINVAL, "invalid input: out_ids needs positions and n_draws >= 1");
+  st = check_params_for(h, rows, vocab);
+  if (st) return st;
+  SmpArgs a = base_args(h, logits, rows, vocab, ld);
+  a.positions = positions;
+  a.n_draws = n_draws < 1 ? 1 : n_draws;
+  a.out_ids = out_ids;
+  bool pen = false;
+  if (aux) {
+    if (aux->n_logprobs < 0 || aux->n_logprobs > KBMAX)
+      return fail(YSKN_SMP_EINVAL, "invalid input: n_logprobs must be in 0..=64");
+    if (aux->n_logprobs > 0 && (!aux->logprob_ids || !aux->logprobs))
+      return fail(YSKN_SMP_EINVAL, "invalid input: n_logprobs > 0 needs both output arrays");
+    if ((aux->top8_ids == nullptr) != (aux->top8_vals == nullptr) ||
+        (aux->top20_ids == nullptr) != (aux->top20_vals == nullptr))
+      return fail(YSKN_SMP_EINVAL, "invalid input: top lists need both ids and values");
+    a.argmax = aux->argmax;
+    a.top8_ids = aux->top8_ids;
+    a.top8_vals = aux->top8_vals;
+    a.top20_ids = aux->top20_ids;
+    a.top20_vals = aux->top20_vals;
+    a.n_lp = aux->n_logprobs;
+    a.lp_ids = aux->logprob_ids;
+    a.lp_vals = aux->logprobs;
+    a.row_status = aux->row_status;
+    a.want_mass = a.n_lp > 0 ? 1 : 0;
+    if (any_penalty(h, rows)) {
+      if (!aux->history || !aux->history_len)
+        return fail(YSKN_SMP_EINVAL, "invalid input: penalties need a history");
+      pen = true;
+    }
+  } else if (any_penalty(h, rows)) {
+    return fail(YSKN_SMP_EINVAL, "invalid input: penalties need a history");
+  }
+  return launch(h, a, dtype, pen, aux, (hipStream_t)stream);
+}
+
+int yskn_smp_argmax(yskn_smp_handle h, const void* logits, int32_t dtype, int32_t rows,
+                    int32_t vocab, int64_t ld, uint32_t* out_ids, void* stream) {
+  int st = check_common(h, logits, dtype, rows, vocab, ld);
+  if (st) return st;
+  if (!out_ids) return fail(YSKN_SMP_EINVAL, "invalid input: null output");
+  SmpArgs a = base_args(h, logits, rows, vocab, ld);
+  a.argmax = out_ids;
+  if (any_penalty(h, rows)) return fail(YSKN_SMP_EINVAL, "invalid input: penalties need yskn_smp_sample");
+  return launch(h, a, dtype, false, nullptr, (hipStream_t)stream);
+}
+
+int yskn_smp_top_tokens(yskn_smp_handle h, const void* logits, int32_t dtype, int32_t rows,
+                        int32_t vocab, int64_t ld, int32_t count, uint32_t* out_ids,
+                        float* out_vals, void* stream) {
+  int st = check_common(h, logits, dtype, rows, vocab, ld);
+  if (st) return st;
+  if (count < 1 || count > KBMAX) return fail(YSKN_SMP_EINVAL, "invalid input: count must be in 1..=64");
+  if (count > vocab) return fail(YSKN_SMP_EINVAL, "invalid input: top-token count exceeds vocabulary");
+  if (!out_ids) return fail(YSKN_SMP_EINVAL, "invalid input: null output");
+  if (any_penalty(h, rows)) return fail(YSKN_SMP_EINVAL, "invalid input: penalties need yskn_smp_sample");
+  SmpArgs a = base_args(h, logits, rows, vocab, ld);
+  a.topn = count;
+  a.topn_ids = out_ids;
+  a.topn_vals = out_vals;
+  return launch(h, a, dtype, false, nullptr, (hipStream_t)stream);
+}
+
+int yskn_smp_nll(yskn_smp_handle h, const void* logits, int32_t dtype, int32_t rows,
+                 int32_t vocab, int64_t ld, const uint32_t* targets, double* out_nll,
+                 void* stream) {
+  int st = check_common(h, logits, dtype, rows, vocab, ld);
+  if (st) return st;
+  if (!targets || !out_nll) return fail(YSKN_SMP_EINVAL, "invalid input: null targets or output");
+  if (any_penalty(h, rows)) return fail(YSKN_SMP_EINVAL, "invalid input: penalties need yskn_smp_sample");
+  SmpArgs a = base_args(h, logits, rows, vocab, ld);
+  a.nll_targets = targets;
+  a.nll_out = out_nll;
+  a.want_mass = 1;
+  return launch(h, a, dtype, false, nullptr, (hipStream_t)stream);
+}
+
+int yskn_smp_verify(yskn_smp_handle h, const void* target_logits, int32_t dtype, int32_t M,
+                    int32_t vocab, int64_t ld, const uint32_t* drafts,
+                    const uint64_t* base_position, const uint32_t* eos_ids, int32_t n_eos,
+                    uint32_t* out_ids, yskn_smp_verify_result* result, void* stream) {
+  int st = check_common(h, target_logits, dtype, M, vocab, ld);
+  if (st) return st;
+  if (!base_position || !out_ids || !result)
+    return fail(YSKN_SMP_EINVAL, "invalid input: null base_position, out_ids or result");
+  if (M > 1 && !drafts) return fail(YSKN_SMP_EINVAL, "invalid input: null drafts");
+  if (n_eos < 0 || (n_eos > 0 && !eos_ids)) return fail(YSKN_SMP_EINVAL, "invalid input: eos ids");
+  if (any_penalty(h, M)) return fail(YSKN_SMP_EINVAL, "invalid input: penalties need yskn_smp_sample");
+  // verification uses the row-0 parameter set for every row
+  const int st2 = validate(h->params[0], vocab, h->flags);
+  if (st2) return st2;
+  SmpArgs a = base_args(h, target_logits, M, vocab, ld);
+  a.prm_shared = 1;
+  a.mode = MODE_VERIFY;
+  a.base_position = base_position;
+  a.out_ids = out_ids;
+  a.drafts = drafts;
+  a.eos = eos_ids;
+  a.n_eos = n_eos;
+  a.vresult = (uint32_t*)result;
+  a.vcount = h->d_vcount;
+  return launch(h, a, dtype, false, nullptr, (hipStream_t)stream);
+}
+
+int yskn_smp_sync(yskn_smp_handle h, void* stream) {
+  if (!h) return fail(YSKN_SMP_EINVAL, "invalid input: null handle");
+  hipError_t e = hipStreamSynchronize((hipStream_t)stream);
+  if (e != hipSuccess) return hip_fail(e, "yskn_smp_sync");
+  std::vector<int32_t> s(h->last_rows > 0 ? h->last_rows : 1, 0);
+  if (h->last_rows > 0) {
+    e = hipMemcpy(s.data(), h->d_status, h->last_rows * sizeof(int32_t), hipMemcpyDeviceToHost);
+    if (e != hipSuccess) return hip_fail(e, "yskn_smp_sync");
+  }
+  for (int32_t v : s) {
+    if (v == YSKN_SMP_ENONFINITE) return fail(v, "non-finite value in logits");
+    if (v == YSKN_SMP_EINVAL) return fail(v, "invalid input: token outside the vocabulary");
+    if (v != YSKN_SMP_OK) return fail(v, "sampler row failed");
+  }
+  return YSKN_SMP_OK;
+}
+
+int yskn_smp_select_host(yskn_smp_handle h, const float* host_logits, int32_t vocab,
+                         uint64_t prediction_position, uint32_t* out_token) {
+  if (!h || !host_logits || !out_token) return fail(YSKN_SMP_EINVAL, "invalid input: null argument");
+  if (vocab <= 0)
+    return fail(YSKN_SMP_EINVAL, "invalid input: logits must contain a nonempty u32-indexed vocabulary");
+  if (vocab > h->max_vocab) return fail(YSKN_SMP_ERANGE, "vocabulary larger than the handle's max_vocab");
+  hipError_t e = hipMemcpy(h->d_host_logits, host_logits, (size_t)vocab * 4, hipMemcpyHostToDevice);
+  if (e == hipSuccess) e = hipMemcpy(h->d_host_pos, &prediction_position, 8, hipMemcpyHostToDevice);
+  if (e != hipSuccess) return hip_fail(e, "yskn_smp_select_host");
+  const bool shared = h->params_shared;
+  int st = check_params_for(h, 1, vocab);
+  if (st) return st;
+  SmpArgs a = base_args(h, h->d_host_logits, 1, vocab, vocab);
+  a.prm_shared = 1;
+  (void)shared;
+  a.positions = h->d_host_pos;
+  a.out_ids = h->d_host_out;
+  if (any_penalty(h, 1)) return fail(YSKN_SMP_EINVAL, "invalid input: penalties need yskn_smp_sample");
+  st = launch(h, a, YSKN_SMP_F32, false, nullptr, nullptr);
+  if (st) return st;
+  st = yskn_smp_sync(h, nullptr);
+  if (st) return st;
+  e = hipMemcpy(out_token, h->d_host_out, 4, hipMemcpyDeviceToHost);
+  if (e != hipSuccess) return hip_fail(e, "yskn_smp_select_host");
+  return YSKN_SMP_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,154 @@
+// smp_internal.hpp -- structures shared by the sampler's kernels and its
+// host-side C ABI. Nothing here crosses the public boundary.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace yskn {
+
+// Launch geometry. One block owns a 16,384-element segment of a row, held in
+// registers (32 elements per thread); a row of V logits spans S = ceil(V/SEG)
+// blocks.
+constexpr int NT = 512;            // threads per block (8 wave64s)
+constexpr int NW = NT / 64;        // waves per block
+constexpr int EPT = 32;            // elements per thread
+constexpr int SEG = NT * EPT;      // elements per block
+constexpr int CAPSEG = 2048;       // candidates a block may hand to its row's finisher
+constexpr int CAP = 2048;          // candidates the finisher sorts in LDS
+constexpr int KBMAX = 64;          // largest "small" top-k / list length
+constexpr int HCAP = 16384;        // history tokens per row for the penalties
+constexpr int MAX_SEGMENTS = 1024; // V <= 16,777,216
+
+// Binary64 log-domain cut for the serial-sum argument: a weight exp_d(z)
+// with z < -37.5 is below 2^-53 and cannot change a running binary64 sum
+// that is already >= 1.
+constexpr double ZCUT = -37.5;
+
+// Segment flags.
+constexpr uint32_t F_NONFINITE = 1u;
+constexpr uint32_t F_OVERFLOW = 2u;
+constexpr uint32_t F_INVALID = 4u;
+constexpr uint32_t F_TIMEOUT = 8u;
+
+// Status codes (public values of include/yskn_smp.h).
+constexpr int32_t ST_OK = 0;
+constexpr int32_t ST_EINVAL = -1;
+constexpr int32_t ST_ENONFINITE = -2;
+
+// Sampling parameters of one row, as the device reads them.
+struct DevParams {
+  double temperature;  // temperature_milli / 1000.0
+  double top_p;        // top_p_milli / 1000.0
+  double min_p;        // min_p_milli / 1000.0
+  uint64_t seed;
+  uint32_t top_k;      // 0 = disabled
+  int32_t version;     // 2 | 3
+  int32_t greedy;      // temperature_milli == 0
+  int32_t penalize;    // any penalty active
+  float rep, pres, freq;
+  int32_t pad;
+};
+
+// What a segment block hands to the row's finisher.
+struct SegInfo {
+  uint64_t maxp;  // packed (key << 32) | ~id of the segment's largest logit
+  double mass;    // sum of exp(l - mref) over the segment (binary32 terms)
+  float mref;     // reference point of mass
+  uint32_t count; // candidates written (<= CAPSEG)
+  uint32_t flags; // F_*
+  uint32_t pad;
+};
+
+// Per-row rendezvous counters; all zero between launches.
+struct RowSync {
+  uint32_t arrive;    // blocks that published their maxima
+  uint32_t done;      // blocks that finished their segment
+  uint32_t hint_max;  // max over published segment max keys
+  uint32_t hint_kb;   // max over published top-KB thresholds
+};
+
+// Counters for profiling the path (cumulative since create).
+enum StatIndex {
+  STAT_ROWS = 0,       // rows finished
+  STAT_DENSE_ROWS,     // rows served by the exact large-candidate path
+  STAT_WAIT_TIMEOUTS,  // segment blocks whose rendezvous timed out
+  STAT_CANDIDATES,     // candidates handed to finishers
+  STAT_COUNT
+};
+
+enum Mode { MODE_SAMPLE = 0, MODE_VERIFY = 1 };
+
+struct SmpArgs {
+  const void* logits;
+  int64_t ld;  // elements between rows
+  int32_t V;
+  int32_t rows;
+  int32_t S;
+  int32_t mode;
+  const DevParams* prm;
+  int32_t prm_shared;
+  int32_t n_draws;
+  const uint64_t* positions;     // [rows * n_draws] (sample mode)
+  const uint64_t* base_position; // verify mode: row j at *base + j + 1
+  uint32_t* out_ids;             // [rows * n_draws] or NULL
+  uint32_t* argmax;
+  uint32_t* top8_ids;
+  float* top8_vals;
+  uint32_t* top20_ids;
+  float* top20_vals;
+  int32_t topn;                  // generic top list (top_tokens API)
+  uint32_t* topn_ids;
+  float* topn_vals;
+  int32_t n_lp;
+  uint32_t* lp_ids;
+  double* lp_vals;
+  const uint32_t* nll_targets;
+  double* nll_out;
+  int32_t want_mass;
+  int32_t* status;       // handle's [rows]
+  int32_t* row_status;   // caller's [rows] or NULL
+  // penalties
+  const uint32_t* pen_bitmap;  // [rows][bm_ld]
+  int64_t bm_ld;
+  const uint32_t* pen_ids;     // [rows][HCAP] sorted unique ids
+  const uint32_t* pen_cnt;     // [rows][HCAP]
+  const int32_t* pen_len;      // [rows], -1 = invalid history
+  // workspace
+  uint64_t* seg_cand;  // [rows][S][CAPSEG]
+  SegInfo* seg_info;   // [rows][S]
+  RowSync* sync;       // [rows]
+  uint64_t* dense_a;   // [rows][dense_ld]
+  uint64_t* dense_b;
+  double* dense_w;
+  int64_t dense_ld;
+  int32_t force_dense;
+  int32_t spin_limit;
+  unsigned long long* stats;
+  // verify
+  const uint32_t* drafts;
+  const uint32_t* eos;
+  int32_t n_eos;
+  uint32_t* vresult;  // 4 words: accepted, emitted, token, stop_eos
+  uint32_t* vcount;
+};
+
+struct PenArgs {
+  const uint32_t* history;
+  const int32_t* history_len;
+  int64_t history_ld;
+  int32_t V;
+  int32_t rows;
+  uint32_t* bitmap;
+  int64_t bm_ld;
+  uint32_t* ids;
+  uint32_t* cnt;
+  int32_t* len;
+  const DevParams* prm;
+  int32_t prm_shared;
+};
+
+// Host-side launchers (smp_kernels.hip).
+hipError_t launch_sample(const SmpArgs& a, int dtype, bool vec, bool pen, hipStream_t st);
+hipError_t launch_penalty_prep(const PenArgs& a, hipStream_t st);
+
+}  // namespace yskn

@@ -1,0 +1,187 @@
+// smp_math.hpp -- bit-exact binary64 exp/log, SplitMix64 mixing and the
+// token-keyed Gumbel noise of YASAKANI's sampler, as gfx950 device code.
+//
+// The algorithms must produce the same bits as the reference's portable
+// math (crates/yskn-ref/src/portable_math.rs:224-364, itself the fdlibm
+// e_exp.c / e_log.c method) and hash (output_head_sampler.rs:214-228).
+// The operation order is therefore fixed by the reference; every binary64
+// multiply, add and divide below is a separately rounded IEEE operation.
+// The translation unit is compiled with -ffp-contract=off so that no
+// multiply/add pair is fused, and division is IEEE correctly rounded.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace yskn {
+
+__device__ __forceinline__ double pm_hilo(uint32_t hi, uint32_t lo) {
+  return __longlong_as_double((long long)(((uint64_t)hi << 32) | (uint64_t)lo));
+}
+__device__ __forceinline__ uint64_t pm_bits(double x) { return (uint64_t)__double_as_longlong(x); }
+
+// exp(value) in binary64; portable_math.rs:224-283.
+__device__ __noinline__ double exp_d(double value) {
+  const uint64_t b = pm_bits(value);
+  const uint32_t hi = (uint32_t)(b >> 32), lo = (uint32_t)b;
+  const bool neg = (hi >> 31) != 0;
+  const uint32_t ahi = hi & 0x7fffffffu;
+  if (ahi >= 0x40862e42u) {
+    if (ahi >= 0x7ff00000u) {
+      if (((ahi & 0x000fffffu) | lo) != 0) return value + value;
+      return neg ? 0.0 : value;
+    }
+    if (value > pm_hilo(0x40862e42u, 0xfefa39efu)) return __longlong_as_double(0x7ff0000000000000ll);
+    if (value < pm_hilo(0xc0874910u, 0xd52d3051u)) return 0.0;
+  }
+  const double ln2_hi = pm_hilo(0x3fe62e42u, 0xfee00000u);
+  const double ln2_lo = pm_hilo(0x3dea39efu, 0x35793c76u);
+  double h = 0.0, l = 0.0, r = value;
+  int32_t k = 0;
+  if (ahi > 0x3fd62e42u) {
+    if (ahi < 0x3ff0a2b2u) {
+      h = value - (neg ? -ln2_hi : ln2_hi);
+      l = neg ? -ln2_lo : ln2_lo;
+      k = neg ? -1 : 1;
+    } else {
+      double t = pm_hilo(0x3ff71547u, 0x652b82feu) * value;
+      t = t + (neg ? -0.5 : 0.5);
+      k = (int32_t)t;  // truncation toward zero; |t| < 1100 here
+      const double kf = (double)k;
+      const double kh = kf * ln2_hi;
+      h = value - kh;
+      l = kf * ln2_lo;
+    }
+    r = h - l;
+  } else if (ahi < 0x3e300000u) {
+    return 1.0 + value;
+  }
+  const double s = r * r;
+  double p = s * pm_hilo(0x3e663769u, 0x72bea4d0u);
+  p = pm_hilo(0xbebbbd41u, 0xc5d26bf1u) + p;
+  p = s * p;
+  p = pm_hilo(0x3f11566au, 0xaf25de2cu) + p;
+  p = s * p;
+  p = pm_hilo(0xbf66c16cu, 0x16bebd93u) + p;
+  p = s * p;
+  p = pm_hilo(0x3fc55555u, 0x5555553eu) + p;
+  const double sp = s * p;
+  const double c = r - sp;
+  const double rc = r * c;
+  if (k == 0) {
+    const double q = rc / (c - 2.0);
+    return 1.0 - (q - r);
+  }
+  const double q = rc / (2.0 - c);
+  const double y = 1.0 - ((l - q) - h);
+  const int32_t adj = (k >= -1021) ? k : k + 1000;
+  const uint64_t yb = pm_bits(y);
+  const uint32_t yhi = (uint32_t)(yb >> 32) + (uint32_t)adj * 1048576u;
+  const double scaled = pm_hilo(yhi, (uint32_t)yb);
+  if (k >= -1021) return scaled;
+  return scaled * pm_hilo(0x01700000u, 0u);
+}
+
+// log(value) in binary64 without a zero special case; portable_math.rs:297-364.
+__device__ __noinline__ double log_d(double value) {
+  int32_t hx = (int32_t)(uint32_t)(pm_bits(value) >> 32);
+  int32_t k = 0;
+  if (hx < 0x00100000) {
+    value = value * pm_hilo(0x43500000u, 0u);
+    k = -54;
+    hx = (int32_t)(uint32_t)(pm_bits(value) >> 32);
+  }
+  k += (hx >> 20) - 1023;
+  hx &= 0x000fffff;
+  const int32_t i = (hx + 0x00095f64) & 0x00100000;
+  value = pm_hilo((uint32_t)(hx | (i ^ 0x3ff00000)), (uint32_t)pm_bits(value));
+  k += i >> 20;
+  const double ln2_hi = pm_hilo(0x3fe62e42u, 0xfee00000u);
+  const double ln2_lo = pm_hilo(0x3dea39efu, 0x35793c76u);
+  const double f = value - 1.0;
+  const double dk = (double)k;
+  if ((0x000fffff & (2 + hx)) < 3) {
+    if (f == 0.0) {
+      if (k == 0) return 0.0;
+      const double a = dk * ln2_hi;
+      const double b2 = dk * ln2_lo;
+      return a + b2;
+    }
+    const double ff = f * f;
+    double t = pm_hilo(0x3fd55555u, 0x55555555u) * f;
+    t = 0.5 - t;
+    const double R = ff * t;
+    if (k == 0) return f - R;
+    const double a = dk * ln2_hi;
+    const double b2 = dk * ln2_lo;
+    return a - ((R - b2) - f);
+  }
+  const double s = f / (2.0 + f);
+  const double z = s * s;
+  const double w = z * z;
+  const int32_t j = (hx - 0x0006147a) | (0x0006b851 - hx);
+  double t2 = w * pm_hilo(0x3fc39a09u, 0xd078c69fu);
+  t2 = pm_hilo(0x3fcc71c5u, 0x1d8e78afu) + t2;
+  t2 = w * t2;
+  t2 = pm_hilo(0x3fd99999u, 0x9997fa04u) + t2;
+  t2 = w * t2;
+  double t1 = w * pm_hilo(0x3fc2f112u, 0xdf3e5244u);
+  t1 = pm_hilo(0x3fc74664u, 0x96cb03deu) + t1;
+  t1 = w * t1;
+  t1 = pm_hilo(0x3fd24924u, 0x94229359u) + t1;
+  t1 = w * t1;
+  t1 = pm_hilo(0x3fe55555u, 0x55555593u) + t1;
+  t1 = z * t1;
+  const double R = t1 + t2;
+  if (j > 0) {
+    double hfsq = 0.5 * f;
+    hfsq = hfsq * f;
+    double u = hfsq + R;
+    u = s * u;
+    if (k == 0) {
+      u = hfsq - u;
+      return f - u;
+    }
+    const double b2 = dk * ln2_lo;
+    u = u + b2;
+    u = hfsq - u;
+    u = u - f;
+    const double a = dk * ln2_hi;
+    return a - u;
+  }
+  double u = f - R;
+  u = s * u;
+  if (k == 0) return f - u;
+  const double b2 = dk * ln2_lo;
+  u = u - b2;
+  u = u - f;
+  const double a = dk * ln2_hi;
+  return a - u;
+}
+
+// SplitMix64 finaliser; output_head_sampler.rs:214-219.
+__device__ __forceinline__ uint64_t mix64(uint64_t z) {
+  z += 0x9e3779b97f4a7c15ull;
+  z = (z ^ (z >> 30)) * 0xbf58476d1ce4e5b9ull;
+  z = (z ^ (z >> 27)) * 0x94d049bb133111ebull;
+  return z ^ (z >> 31);
+}
+
+// Token-keyed Gumbel noise given the per-(seed, position) hash
+// b = mix64(mix64(seed) ^ position); output_head_sampler.rs:221-228.
+__device__ __forceinline__ double gumbel_from_key(uint64_t b, uint32_t token) {
+  const uint64_t h = mix64(b ^ ((uint64_t)token * 0xd6e8feb86659fd93ull));
+  double u = (double)(h >> 11) + 0.5;
+  u = u * (1.0 / 9007199254740992.0);
+  return -log_d(-log_d(u));
+}
+
+__device__ __forceinline__ uint64_t position_key(uint64_t seed, uint64_t position) {
+  return mix64(mix64(seed) ^ position);
+}
+
+// Version-2 uniform; output_head_sampler.rs:196-197 (no +0.5).
+__device__ __forceinline__ double uniform_v2(uint64_t seed, uint64_t position) {
+  return (double)(position_key(seed, position) >> 11) * (1.0 / 9007199254740992.0);
+}
+
+}  // namespace yskn

@@ -1,0 +1,410 @@
+"""Python host binding of the MI355X sampling library (include/yskn_smp.h).
+
+The names mirror the reference's sampling surface so that callers and tests
+read like the reference's own:
+
+* ``SamplingParameters`` / ``SamplingParameters.from_thousandths`` /
+  ``validate``  -- crates/yskn-ref/src/output_head_sampler.rs:21-75
+* ``Sampler`` with ``Greedy`` and ``Sampled(params)`` and ``sample(logits,
+  prediction_position)`` -- output_head_sampler.rs:77-92
+* ``greedy``, ``top_tokens``, ``negative_log_likelihood`` --
+  output_head_sampler.rs:103-134,230-250
+* ``select`` (the ``Selector`` trait, crates/yskn-ref/src/speculation.rs:121-131)
+* ``verify`` -- the acceptance loop of speculation.rs:483-523
+
+Errors are raised as ``InvalidInput`` / ``NonFinite`` (lib.rs:37-45).
+
+Every call goes through the HIP library ``lib/libyskn_smp.so``; there is no
+CPU fallback. If the library is missing the import of the binding fails.
+PyTorch provides device memory and the stream only.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+from dataclasses import dataclass, field
+from typing import Optional, Sequence
+
+import numpy as np
+
+PKG_ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+LIB_PATH = os.path.join(PKG_ROOT, "lib", "libyskn_smp.so")
+
+OK, EINVAL, ENONFINITE, ERANGE, EDEVICE = 0, -1, -2, -3, -4
+F32, BF16 = 0, 1
+INVERSE_CUMULATIVE, GUMBEL = 2, 3
+FLAG_EXTENDED_TOP_K, FLAG_FORCE_DENSE = 0x1, 0x2
+
+
+class SamplerError(Exception):
+    """Base error; ``code`` is the C-ABI status."""
+
+    def __init__(self, code: int, message: str):
+        super().__init__(message)
+        self.code = code
+
+
+class InvalidInput(SamplerError):
+    pass
+
+
+class NonFinite(SamplerError):
+    pass
+
+
+class DeviceError(SamplerError):
+    pass
+
+
+class CParams(C.Structure):
+    _fields_ = [
+        ("temperature_milli", C.c_uint32),
+        ("top_p_milli", C.c_uint32),
+        ("top_k", C.c_uint32),
+        ("min_p_milli", C.c_uint32),
+        ("seed", C.c_uint64),
+        ("version", C.c_int32),
+        ("repetition_penalty", C.c_float),
+        ("presence_penalty", C.c_float),
+        ("frequency_penalty", C.c_float),
+    ]
+
+
+class CAux(C.Structure):
+    _fields_ = [
+        ("argmax", C.c_void_p),
+        ("top8_ids", C.c_void_p),
+        ("top8_vals", C.c_void_p),
+        ("top20_ids", C.c_void_p),
+        ("top20_vals", C.c_void_p),
+        ("n_logprobs", C.c_int32),
+        ("logprob_ids", C.c_void_p),
+        ("logprobs", C.c_void_p),
+        ("row_status", C.c_void_p),
+        ("history", C.c_void_p),
+        ("history_len", C.c_void_p),
+        ("history_ld", C.c_int64),
+    ]
+
+
+EXPORTED = [
+    "yskn_smp_last_error", "yskn_smp_create", "yskn_smp_destroy", "yskn_smp_set_params",
+    "yskn_smp_sample", "yskn_smp_argmax", "yskn_smp_top_tokens", "yskn_smp_nll",
+    "yskn_smp_verify", "yskn_smp_sync", "yskn_smp_select_host", "yskn_smp_validate_params",
+    "yskn_smp_version",
+]
+
+_lib = None
+
+
+def load_library(path: str = LIB_PATH) -> C.CDLL:
+    """Load libyskn_smp.so (raises if it has not been built)."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(path):
+        raise RuntimeError(f"{path} is not built; run __graft_entry__.build()")
+    L = C.CDLL(path)
+    vp, i32, i64, u32, u64 = C.c_void_p, C.c_int32, C.c_int64, C.c_uint32, C.c_uint64
+    L.yskn_smp_last_error.restype = C.c_char_p
+    L.yskn_smp_version.restype = C.c_char_p
+    L.yskn_smp_create.argtypes = [i32, i32, u32, C.POINTER(vp)]
+    L.yskn_smp_destroy.argtypes = [vp]
+    L.yskn_smp_destroy.restype = None
+    L.yskn_smp_set_params.argtypes = [vp, C.POINTER(CParams), i32]
+    L.yskn_smp_sample.argtypes = [vp, vp, i32, i32, i32, i64, vp, i32, vp, C.POINTER(CAux), vp]
+    L.yskn_smp_argmax.argtypes = [vp, vp, i32, i32, i32, i64, vp, vp]
+    L.yskn_smp_top_tokens.argtypes = [vp, vp, i32, i32, i32, i64, i32, vp, vp, vp]
+    L.yskn_smp_nll.argtypes = [vp, vp, i32, i32, i32, i64, vp, vp, vp]
+    L.yskn_smp_verify.argtypes = [vp, vp, i32, i32, i32, i64, vp, vp, vp, i32, vp, vp, vp]
+    L.yskn_smp_sync.argtypes = [vp, vp]
+    L.yskn_smp_select_host.argtypes = [vp, vp, i32, u64, C.POINTER(u32)]
+    L.yskn_smp_validate_params.argtypes = [C.POINTER(CParams), i32, u32]
+    for name in ("yskn_smp_create", "yskn_smp_set_params", "yskn_smp_sample", "yskn_smp_argmax",
+                 "yskn_smp_top_tokens", "yskn_smp_nll", "yskn_smp_verify", "yskn_smp_sync",
+                 "yskn_smp_select_host", "yskn_smp_validate_params"):
+        L[name].restype = C.c_int
+    _lib = L
+    return L
+
+
+def _raise(code: int) -> None:
+    if code == OK:
+        return
+    msg = (_lib.yskn_smp_last_error() or b"").decode()
+    if code == ENONFINITE:
+        raise NonFinite(code, msg)
+    if code in (EINVAL, ERANGE):
+        raise InvalidInput(code, msg)
+    raise DeviceError(code, msg)
+
+
+@dataclass
+class SamplingParameters:
+    """Integer-thousandths sampling parameters (the native setter's units,
+    src/engine35.cpp:946-959); the sampler stores binary64 value / 1000.0.
+    temperature_milli = 0 selects greedy."""
+
+    temperature_milli: int = 1000
+    top_p_milli: int = 950
+    top_k: int = 20
+    min_p_milli: int = 0
+    seed: int = 0
+    version: int = GUMBEL
+    repetition_penalty: float = 1.0
+    presence_penalty: float = 0.0
+    frequency_penalty: float = 0.0
+
+    @classmethod
+    def from_thousandths(cls, temperature: int, top_p: int, min_p: int) -> "SamplingParameters":
+        p = cls(temperature_milli=temperature, top_p_milli=top_p, min_p_milli=min_p)
+        p.validate(20)
+        return p
+
+    @property
+    def temperature(self) -> float:
+        return self.temperature_milli / 1000.0
+
+    @property
+    def top_p(self) -> float:
+        return self.top_p_milli / 1000.0
+
+    @property
+    def min_p(self) -> float:
+        return self.min_p_milli / 1000.0
+
+    def to_c(self) -> CParams:
+        return CParams(self.temperature_milli, self.top_p_milli, self.top_k, self.min_p_milli,
+                       self.seed & 0xFFFFFFFFFFFFFFFF, self.version, self.repetition_penalty,
+                       self.presence_penalty, self.frequency_penalty)
+
+    def validate(self, vocabulary_size: int, flags: int = 0) -> None:
+        L = load_library()
+        c = self.to_c()
+        _raise(L.yskn_smp_validate_params(C.byref(c), vocabulary_size, flags))
+
+
+def _ptr(t) -> Optional[int]:
+    return None if t is None else t.data_ptr()
+
+
+class DeviceSampler:
+    """Owns one native handle: scratch for up to ``max_rows`` rows of up to
+    ``max_vocab`` logits. Calls are asynchronous on the current torch stream;
+    ``sync()`` raises the first per-row error of the last call."""
+
+    def __init__(self, max_rows: int, max_vocab: int, extended_top_k: bool = False,
+                 force_dense: bool = False):
+        import torch  # device memory and streams only
+
+        self.torch = torch
+        self.L = load_library()
+        flags = (FLAG_EXTENDED_TOP_K if extended_top_k else 0) | (FLAG_FORCE_DENSE if force_dense else 0)
+        self.flags = flags
+        h = C.c_void_p()
+        _raise(self.L.yskn_smp_create(max_rows, max_vocab, flags, C.byref(h)))
+        self.h = h
+        self.max_rows, self.max_vocab = max_rows, max_vocab
+        self.device = torch.device("cuda", torch.cuda.current_device())
+
+    def close(self) -> None:
+        if getattr(self, "h", None):
+            self.L.yskn_smp_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def _stream(self):
+        return C.c_void_p(self.torch.cuda.current_stream().cuda_stream)
+
+    def set_params(self, params) -> None:
+        if isinstance(params, SamplingParameters):
+            params = [params]
+        arr = (CParams * len(params))(*[p.to_c() for p in params])
+        _raise(self.L.yskn_smp_set_params(self.h, arr, len(params)))
+
+    @staticmethod
+    def _dtype(logits) -> int:
+        import torch
+
+        if logits.dtype == torch.float32:
+            return F32
+        if logits.dtype == torch.bfloat16:
+            return BF16
+        raise InvalidInput(EINVAL, "logits must be float32 or bfloat16")
+
+    def _check_logits(self, logits):
+        if not logits.is_cuda or logits.dim() != 2 or logits.stride(1) != 1:
+            raise InvalidInput(EINVAL, "logits must be a 2-D CUDA tensor with unit column stride")
+        return logits.shape[0], logits.shape[1], logits.stride(0)
+
+    def sample(self, logits, positions, *, argmax=False, top8=False, top20=False,
+               n_logprobs=0, history=None, history_len=None, row_status=False):
+        """Sample; positions is an int64 tensor [rows] or [rows, n_draws] of
+        absolute prediction positions. Returns a dict of device tensors."""
+        torch = self.torch
+        rows, V, ld = self._check_logits(logits)
+        pos = positions.to(torch.int64)
+        if pos.dim() == 1:
+            pos = pos.reshape(rows, 1)
+        pos = pos.contiguous()
+        n_draws = pos.shape[1]
+        dev = logits.device
+        out = {"ids": torch.empty((rows, n_draws), dtype=torch.int32, device=dev)}
+        aux = CAux()
+        if argmax:
+            out["argmax"] = torch.empty(rows, dtype=torch.int32, device=dev)
+            aux.argmax = out["argmax"].data_ptr()
+        if top8:
+            out["top8_ids"] = torch.empty((rows, 8), dtype=torch.int32, device=dev)
+            out["top8_vals"] = torch.empty((rows, 8), dtype=torch.float32, device=dev)
+            aux.top8_ids, aux.top8_vals = out["top8_ids"].data_ptr(), out["top8_vals"].data_ptr()
+        if top20:
+            out["top20_ids"] = torch.empty((rows, 20), dtype=torch.int32, device=dev)
+            out["top20_vals"] = torch.empty((rows, 20), dtype=torch.float32, device=dev)
+            aux.top20_ids, aux.top20_vals = out["top20_ids"].data_ptr(), out["top20_vals"].data_ptr()
+        if n_logprobs:
+            out["logprob_ids"] = torch.empty((rows, n_logprobs), dtype=torch.int32, device=dev)
+            out["logprobs"] = torch.empty((rows, n_logprobs), dtype=torch.float64, device=dev)
+            aux.n_logprobs = n_logprobs
+            aux.logprob_ids, aux.logprobs = out["logprob_ids"].data_ptr(), out["logprobs"].data_ptr()
+        if row_status:
+            out["status"] = torch.empty(rows, dtype=torch.int32, device=dev)
+            aux.row_status = out["status"].data_ptr()
+        if history is not None:
+            hist = history.to(torch.int32).contiguous()
+            if hist.dim() == 1:
+                hist = hist.reshape(1, -1)
+            hl = history_len
+            if hl is None:
+                hl = torch.full((rows,), hist.shape[1], dtype=torch.int32, device=dev)
+            hl = hl.to(torch.int32).contiguous()
+            out["_hist"], out["_hl"] = hist, hl
+            aux.history, aux.history_len, aux.history_ld = hist.data_ptr(), hl.data_ptr(), hist.stride(0)
+        out["_pos"] = pos
+        _raise(self.L.yskn_smp_sample(self.h, logits.data_ptr(), self._dtype(logits), rows, V, ld,
+                                      pos.data_ptr(), n_draws, out["ids"].data_ptr(),
+                                      C.byref(aux), self._stream()))
+        return out
+
+    def argmax(self, logits):
+        torch = self.torch
+        rows, V, ld = self._check_logits(logits)
+        out = torch.empty(rows, dtype=torch.int32, device=logits.device)
+        _raise(self.L.yskn_smp_argmax(self.h, logits.data_ptr(), self._dtype(logits), rows, V, ld,
+                                      out.data_ptr(), self._stream()))
+        return out
+
+    def top_tokens(self, logits, count: int):
+        torch = self.torch
+        rows, V, ld = self._check_logits(logits)
+        ids = torch.empty((rows, count), dtype=torch.int32, device=logits.device)
+        vals = torch.empty((rows, count), dtype=torch.float32, device=logits.device)
+        _raise(self.L.yskn_smp_top_tokens(self.h, logits.data_ptr(), self._dtype(logits), rows, V,
+                                          ld, count, ids.data_ptr(), vals.data_ptr(),
+                                          self._stream()))
+        return ids, vals
+
+    def nll(self, logits, targets):
+        torch = self.torch
+        rows, V, ld = self._check_logits(logits)
+        t = targets.to(torch.int32).contiguous()
+        out = torch.empty(rows, dtype=torch.float64, device=logits.device)
+        _raise(self.L.yskn_smp_nll(self.h, logits.data_ptr(), self._dtype(logits), rows, V, ld,
+                                   t.data_ptr(), out.data_ptr(), self._stream()))
+        return out
+
+    def verify(self, logits, drafts, base_position, eos_ids: Sequence[int] = ()):
+        """One-launch verification of M rows; returns (ids[M], result[4]) device
+        tensors: result = (accepted, emitted, token, stop_eos)."""
+        torch = self.torch
+        M, V, ld = self._check_logits(logits)
+        dev = logits.device
+        d = drafts.to(torch.int32).contiguous() if M > 1 else torch.zeros(1, dtype=torch.int32, device=dev)
+        bp = base_position.to(torch.int64).reshape(1).contiguous()
+        eos = torch.tensor(list(eos_ids) or [0], dtype=torch.int32, device=dev)
+        ids = torch.empty(M, dtype=torch.int32, device=dev)
+        res = torch.empty(4, dtype=torch.int32, device=dev)
+        _raise(self.L.yskn_smp_verify(self.h, logits.data_ptr(), self._dtype(logits), M, V, ld,
+                                      d.data_ptr(), bp.data_ptr(), eos.data_ptr(), len(eos_ids),
+                                      ids.data_ptr(), res.data_ptr(), self._stream()))
+        return ids, res, (d, bp, eos)
+
+    def sync(self) -> None:
+        _raise(self.L.yskn_smp_sync(self.h, self._stream()))
+
+    def select(self, logits: np.ndarray, prediction_position: int) -> int:
+        """Selector::select on a host slice (speculation.rs:121-131)."""
+        a = np.ascontiguousarray(logits, dtype=np.float32)
+        out = C.c_uint32()
+        _raise(self.L.yskn_smp_select_host(self.h, a.ctypes.data, a.size, prediction_position,
+                                           C.byref(out)))
+        return out.value
+
+
+@dataclass
+class Sampler:
+    """``Sampler::{Greedy, Sampled(params)}`` (output_head_sampler.rs:77-92)
+    running on the device. ``sample`` takes a host slice, like the Rust API."""
+
+    params: Optional[SamplingParameters] = None  # None = Greedy
+    extended_top_k: bool = False
+    _dev: Optional[DeviceSampler] = field(default=None, repr=False)
+
+    @classmethod
+    def greedy(cls) -> "Sampler":
+        return cls(None)
+
+    @classmethod
+    def sampled(cls, params: SamplingParameters, extended_top_k: bool = False) -> "Sampler":
+        return cls(params, extended_top_k)
+
+    def _device(self, V: int) -> DeviceSampler:
+        if self._dev is None or self._dev.max_vocab < V:
+            self._dev = DeviceSampler(1, max(V, 1), extended_top_k=self.extended_top_k)
+        self._dev.set_params(self.params if self.params is not None
+                             else SamplingParameters(temperature_milli=0))
+        return self._dev
+
+    def sample(self, logits, prediction_position: int) -> int:
+        a = np.ascontiguousarray(logits, dtype=np.float32)
+        if a.size == 0:
+            load_library()
+            raise InvalidInput(EINVAL, "invalid input: logits must contain a nonempty u32-indexed vocabulary")
+        return self._device(a.size).select(a, prediction_position)
+
+    select = sample
+
+
+def greedy(logits) -> int:
+    return Sampler.greedy().sample(logits, 0)
+
+
+def top_tokens(logits, count: int) -> np.ndarray:
+    import torch
+
+    a = np.ascontiguousarray(logits, dtype=np.float32)
+    dev = DeviceSampler(1, max(a.size, 1))
+    t = torch.from_numpy(a).reshape(1, -1).cuda()
+    ids, _ = dev.top_tokens(t, count)
+    dev.sync()
+    return ids.cpu().numpy().astype(np.uint32).reshape(-1)
+
+
+def negative_log_likelihood(logits, target: int) -> float:
+    import torch
+
+    a = np.ascontiguousarray(logits, dtype=np.float32)
+    dev = DeviceSampler(1, max(a.size, 1))
+    t = torch.from_numpy(a).reshape(1, -1).cuda()
+    out = dev.nll(t, torch.tensor([target], dtype=torch.int32, device=t.device))
+    dev.sync()
+    return float(out.cpu()[0])
+
+
+def version() -> str:
+    return load_library().yskn_smp_version().decode()
