@@ -127,6 +127,7 @@ def main():
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
     smp.sync()
+    stats = smp.stats()
     per_launch_ms = np.array([s.elapsed_time(e) for s, e in ev])
     avg_launch_s = float(per_launch_ms.mean()) / 1e3
     ms_per_step = wall * 1e3 / a.steps
@@ -170,6 +171,7 @@ def main():
                      "kernel_us": avg_launch_s * 1e6},
         "cpu_baseline": cpu,
         "parity_with_oracle": parity,
+        "path_stats": stats,
     }
     print(json.dumps(res))
 

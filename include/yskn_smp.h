@@ -148,7 +148,9 @@ int yskn_smp_sample(yskn_smp_handle h, const void* logits, int32_t dtype, int32_
                     uint32_t* out_ids, const yskn_smp_aux* aux, void* stream);
 
 /* Greedy argmax per row: greedy() (output_head_sampler.rs:103-113),
- * launch_argmax (src/args.hpp:24-30; src/misc_kernels.cu:57-96). */
+ * launch_argmax (src/args.hpp:24-30; src/misc_kernels.cu:57-96).
+ * Like the two entry points below, a pure function of the logits: the
+ * handle's sampling parameters (penalties included) are not used. */
 int yskn_smp_argmax(yskn_smp_handle h, const void* logits, int32_t dtype, int32_t rows,
                     int32_t vocab, int64_t ld, uint32_t* out_ids, void* stream);
 
@@ -190,6 +192,14 @@ int yskn_smp_sync(yskn_smp_handle h, void* stream);
  * the device, samples with row-0 parameters, returns the token synchronously. */
 int yskn_smp_select_host(yskn_smp_handle h, const float* host_logits, int32_t vocab,
                          uint64_t prediction_position, uint32_t* out_token);
+
+/* Profiling counters of the handle, cumulative since create (no counterpart
+ * in the reference, which has no sampler-level instrumentation): out[0] rows
+ * finished, out[1] rows served by the exact large-candidate path, out[2] rows
+ * whose segment rendezvous timed out, out[3] candidates handed to row
+ * finishers, out[4] rendezvous polling iterations. Synchronises the device.
+ * Returns the number of counters written (<= n) or a negative status. */
+int yskn_smp_get_stats(yskn_smp_handle h, uint64_t* out, int32_t n);
 
 /* Validate parameters on the host without a device (the reference's
  * SamplingParameters::validate, output_head_sampler.rs:56-75). */

@@ -8,6 +8,7 @@
 #include <hip/hip_runtime.h>
 
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <string>
 #include <vector>
@@ -65,6 +66,7 @@ struct yskn_smp {
   uint64_t* d_host_pos = nullptr;
   uint32_t* d_host_out = nullptr;
   int32_t last_rows = 0;
+  int32_t spin_limit = SPIN_LIMIT;
 };
 
 namespace {
@@ -198,7 +200,7 @@ SmpArgs base_args(yskn_smp_handle h, const void* logits, int32_t rows, int32_t v
   a.dense_w = h->d_dense_w;
   a.dense_ld = h->dense_ld;
   a.force_dense = (h->flags & YSKN_SMP_FLAG_FORCE_DENSE) ? 1 : 0;
-  a.spin_limit = SPIN_LIMIT;
+  a.spin_limit = h->spin_limit;
   a.stats = h->d_stats;
   return a;
 }
@@ -263,6 +265,9 @@ int yskn_smp_create(int32_t max_rows, int32_t max_vocab, uint32_t flags, yskn_sm
   h->max_segments = (max_vocab + SEG - 1) / SEG;
   h->params.assign(1, default_params());
   h->params_shared = true;
+  // YSKN_SMP_SPIN_LIMIT bounds the rendezvous polling (0 disables waiting;
+  // results are identical, only the candidate filter is weaker).
+  if (const char* e = std::getenv("YSKN_SMP_SPIN_LIMIT")) h->spin_limit = std::atoi(e);
   if (hipGetDevice(&h->device) != hipSuccess) h->device = 0;
   const size_t R = (size_t)max_rows, Sg = (size_t)h->max_segments;
   h->dense_ld = ((int64_t)max_vocab + 63) / 64 * 64;
@@ -389,7 +394,6 @@ int yskn_smp_argmax(yskn_smp_handle h, const void* logits, int32_t dtype, int32_
   if (!out_ids) return fail(YSKN_SMP_EINVAL, "invalid input: null output");
   SmpArgs a = base_args(h, logits, rows, vocab, ld);
   a.argmax = out_ids;
-  if (any_penalty(h, rows)) return fail(YSKN_SMP_EINVAL, "invalid input: penalties need yskn_smp_sample");
   return launch(h, a, dtype, false, nullptr, (hipStream_t)stream);
 }
 
@@ -401,7 +405,6 @@ int yskn_smp_top_tokens(yskn_smp_handle h, const void* logits, int32_t dtype, in
   if (count < 1 || count > KBMAX) return fail(YSKN_SMP_EINVAL, "invalid input: count must be in 1..=64");
   if (count > vocab) return fail(YSKN_SMP_EINVAL, "invalid input: top-token count exceeds vocabulary");
   if (!out_ids) return fail(YSKN_SMP_EINVAL, "invalid input: null output");
-  if (any_penalty(h, rows)) return fail(YSKN_SMP_EINVAL, "invalid input: penalties need yskn_smp_sample");
   SmpArgs a = base_args(h, logits, rows, vocab, ld);
   a.topn = count;
   a.topn_ids = out_ids;
@@ -415,7 +418,6 @@ int yskn_smp_nll(yskn_smp_handle h, const void* logits, int32_t dtype, int32_t r
   int st = check_common(h, logits, dtype, rows, vocab, ld);
   if (st) return st;
   if (!targets || !out_nll) return fail(YSKN_SMP_EINVAL, "invalid input: null targets or output");
-  if (any_penalty(h, rows)) return fail(YSKN_SMP_EINVAL, "invalid input: penalties need yskn_smp_sample");
   SmpArgs a = base_args(h, logits, rows, vocab, ld);
   a.nll_targets = targets;
   a.nll_out = out_nll;
@@ -465,6 +467,17 @@ int yskn_smp_sync(yskn_smp_handle h, void* stream) {
     if (v != YSKN_SMP_OK) return fail(v, "sampler row failed");
   }
   return YSKN_SMP_OK;
+}
+
+int yskn_smp_get_stats(yskn_smp_handle h, uint64_t* out, int32_t n) {
+  if (!h || !out || n < 0) return fail(YSKN_SMP_EINVAL, "invalid input: null handle or output");
+  unsigned long long v[STAT_COUNT];
+  hipError_t e = hipDeviceSynchronize();
+  if (e == hipSuccess) e = hipMemcpy(v, h->d_stats, sizeof v, hipMemcpyDeviceToHost);
+  if (e != hipSuccess) return hip_fail(e, "yskn_smp_get_stats");
+  const int m = n < STAT_COUNT ? n : STAT_COUNT;
+  for (int i = 0; i < m; ++i) out[i] = v[i];
+  return m;
 }
 
 int yskn_smp_select_host(yskn_smp_handle h, const float* host_logits, int32_t vocab,

@@ -56,7 +56,7 @@ struct SegInfo {
   float mref;     // reference point of mass
   uint32_t count; // candidates written (<= CAPSEG)
   uint32_t flags; // F_*
-  uint32_t pad;
+  uint32_t th1;   // the block's top-KB threshold key
 };
 
 // Per-row rendezvous counters; all zero between launches.
@@ -73,6 +73,7 @@ enum StatIndex {
   STAT_DENSE_ROWS,     // rows served by the exact large-candidate path
   STAT_WAIT_TIMEOUTS,  // segment blocks whose rendezvous timed out
   STAT_CANDIDATES,     // candidates handed to finishers
+  STAT_SPINS,          // rendezvous polling iterations over all blocks
   STAT_COUNT
 };
 

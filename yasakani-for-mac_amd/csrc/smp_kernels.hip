@@ -1,13 +1,14 @@
 // smp_kernels.hip -- gfx950 kernels of the per-step sampling path.
 //
-// One launch per call. Grid (S, rows): block (seg, row) owns 16,384 logits of
+// One launch per call. S * rows blocks: block (seg, row) owns 16,384 logits of
 // the row in registers (32 per thread, coalesced 16-byte loads). The path:
 //
 //  1. scan: order-preserving 32-bit keys, segment max, non-finite check.
-//  2. rendezvous: each block publishes its max key and a top-KB threshold
-//     with agent-scope atomics and waits, with a bounded spin that always
-//     ends, until every block of its row has published. Every block then
-//     knows the row maximum M (or a lower bound of it after a time-out).
+//  2. row bounds: each block publishes its max key and a top-KB threshold
+//     with agent-scope atomic max operations, whose return values give it
+//     the row's running maxima at once. A block that would keep too many
+//     elements under those bounds waits, with a bounded spin that always
+//     ends, until every block of its row has published.
 //  3. filter: a block keeps only elements that can matter to the reference
 //     algorithm: (a) elements whose binary64 weight exp_d((l - M)/T) can
 //     reach 2^-53 -- smaller weights are absorbed by the reference's serial
@@ -509,8 +510,25 @@ __global__ __launch_bounds__(NT) void smp_main(SmpArgs A) {
   __shared__ TailShared ts;
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int seg = blockIdx.x, row = blockIdx.y;
   const int S = A.S;
+  // Workgroups are dealt round-robin to the 8 XCDs (linear id mod 8). Groups
+  // of 8 rows are laid out so that all S segments of a row share one XCD:
+  // its segments are dispatched together by one dispatcher and the row's
+  // hand-off traffic stays within one L2.
+  int row, seg;
+  {
+    const int b = blockIdx.x;
+    const int full = (A.rows / 8) * 8;  // rows in complete groups of 8
+    if (b < full * S) {
+      const int g = b / (8 * S), r8 = b - g * 8 * S;
+      row = g * 8 + (r8 & 7);
+      seg = r8 >> 3;
+    } else {
+      const int r = b - full * S;
+      row = full + r / S;
+      seg = r - (r / S) * S;
+    }
+  }
   const int32_t V = A.V;
   const DevParams P = A.prm[A.prm_shared ? 0 : row];
   const RowPlan plan = make_plan(A, P);
@@ -610,38 +628,70 @@ __global__ __launch_bounds__(NT) void smp_main(SmpArgs A) {
 #pragma unroll
   for (int w = 1; w < NW; ++w) th1 = th1 < red_u32[w] ? th1 : red_u32[w];
 
-  // ---- 2. row rendezvous (bounded wait) ----------------------------------
+  // ---- 2. row bounds -------------------------------------------------------
+  // Each block publishes its max key and its top-KB threshold; fetch_max
+  // returns the row's running maxima, so a block obtains bounds without
+  // waiting. Only monotone bounds travel this way: any value read is a valid
+  // (if weaker) bound, so relaxed atomics suffice and no cache-wide fence is
+  // issued while blocks stream their segments.
   if (tid == 0) {
     RowSync* rs = A.sync + row;
-    __hip_atomic_fetch_max(&rs->hint_max, key_b, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    __hip_atomic_fetch_max(&rs->hint_kb, th1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    __hip_atomic_fetch_add(&rs->arrive, 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
-    uint32_t n = 0;
-    for (int it = 0; it < A.spin_limit; ++it) {
-      n = __hip_atomic_load(&rs->arrive, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_AGENT);
-      if (n >= (uint32_t)S) break;
-      __builtin_amdgcn_s_sleep(4);
-    }
-    const uint32_t hm = __hip_atomic_load(&rs->hint_max, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    const uint32_t hk = __hip_atomic_load(&rs->hint_kb, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    bc[0] = hm > key_b ? hm : key_b;
-    bc[1] = hk > th1 ? hk : th1;
-    bc[2] = n >= (uint32_t)S ? 0u : F_TIMEOUT;
+    const uint32_t om = __hip_atomic_fetch_max(&rs->hint_max, key_b, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const uint32_t ok = __hip_atomic_fetch_max(&rs->hint_kb, th1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_fetch_add(&rs->arrive, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    bc[0] = om > key_b ? om : key_b;
+    bc[1] = ok > th1 ? ok : th1;
+    bc[2] = 0u;
   }
   __syncthreads();
-  const uint32_t mkey = bc[0];
-  const uint32_t th_kb = bc[1];
-  seg_flags |= bc[2];
-  const float m_ref = key2f(mkey);
+  uint32_t mkey = bc[0];
+  uint32_t th_kb = bc[1];
+  float m_ref = key2f(mkey);
 
   // ---- 3. filter --------------------------------------------------------
-  uint32_t theta = th_kb;
-  if (plan.need_rel) {
-    const uint32_t tr = relevance_key(m_ref, P.temperature);
-    theta = tr < theta ? tr : theta;
+  auto threshold = [&](float mr, uint32_t kb) {
+    uint32_t t = kb;
+    if (plan.need_rel) {
+      const uint32_t tr = relevance_key(mr, P.temperature);
+      t = tr < t ? tr : t;
+    }
+    if (A.force_dense) t = 0xffffffffu;  // compact path unused
+    return t < 1u ? 1u : t;
+  };
+  uint32_t theta = threshold(m_ref, th_kb);
+  int cnt = 0;
+#pragma unroll
+  for (int i = 0; i < EPT; ++i) cnt += (key[i] >= theta) ? 1 : 0;
+  int total = block_sum_int(cnt, red_int);
+  if (total > CAPSEG / 2 && A.spin_limit > 0) {
+    // Too many survivors under the bounds seen so far: wait (bounded) until
+    // every block of the row has published, then filter again.
+    if (tid == 0) {
+      RowSync* rs = A.sync + row;
+      uint32_t n = 0;
+      int it = 0;
+      for (; it < A.spin_limit; ++it) {
+        n = __hip_atomic_load(&rs->arrive, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (n >= (uint32_t)S) break;
+        __builtin_amdgcn_s_sleep(2);
+      }
+      if (A.stats) atomicAdd(&A.stats[STAT_SPINS], (unsigned long long)it + 1ull);
+      const uint32_t hm = __hip_atomic_load(&rs->hint_max, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      const uint32_t hk = __hip_atomic_load(&rs->hint_kb, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      bc[3] = hm > mkey ? hm : mkey;
+      bc[4] = hk > th_kb ? hk : th_kb;
+      bc[2] = n >= (uint32_t)S ? 0u : F_TIMEOUT;
+    }
+    __syncthreads();
+    mkey = bc[3];
+    th_kb = bc[4];
+    m_ref = key2f(mkey);
+    theta = threshold(m_ref, th_kb);
+    cnt = 0;
+#pragma unroll
+    for (int i = 0; i < EPT; ++i) cnt += (key[i] >= theta) ? 1 : 0;
   }
-  if (A.force_dense) theta = 0xffffffffu;  // compact path unused; keep the segment max only
-  if (theta < 1u) theta = 1u;
+  seg_flags |= bc[2];
 
   // mass relative to m_ref: binary32 terms, pairwise within the thread
   double mass = 0.0;
@@ -661,10 +711,6 @@ __global__ __launch_bounds__(NT) void smp_main(SmpArgs A) {
     mass = block_sum_f64((double)acc[0], red_f64);
   }
 
-  int cnt = 0;
-#pragma unroll
-  for (int i = 0; i < EPT; ++i) cnt += (key[i] >= theta) ? 1 : 0;
-  int total;
   const int off = block_excl_scan(cnt, red_int, &total);
   const bool overflow = total > CAPSEG;
   if (!overflow && cnt) {
@@ -689,21 +735,23 @@ __global__ __launch_bounds__(NT) void smp_main(SmpArgs A) {
     si.mref = m_ref;
     si.count = overflow ? 0u : (uint32_t)total;
     si.flags = seg_flags | (overflow ? F_OVERFLOW : 0u);
-    si.pad = 0;
+    si.th1 = th1;
     A.seg_info[(int64_t)row * S + seg] = si;
   }
 
   // ---- last block of the row finishes ------------------------------------
-  __threadfence();
+  // release: this block's candidates and SegInfo reach device-coherent memory
+  // before its arrival is counted; the finisher acquires once.
   __syncthreads();
   if (tid == 0) {
-    const uint32_t old = __hip_atomic_fetch_add(&A.sync[row].done, 1u, __ATOMIC_ACQ_REL,
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+    const uint32_t old = __hip_atomic_fetch_add(&A.sync[row].done, 1u, __ATOMIC_RELAXED,
                                                 __HIP_MEMORY_SCOPE_AGENT);
-    bc[3] = (old == (uint32_t)(S - 1)) ? 1u : 0u;
+    bc[5] = (old == (uint32_t)(S - 1)) ? 1u : 0u;
+    if (bc[5]) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
   }
   __syncthreads();
-  if (!bc[3]) return;
-  __threadfence();
+  if (!bc[5]) return;
   if (tid == 0) {
     RowSync* rs = A.sync + row;
     __hip_atomic_store(&rs->arrive, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -713,29 +761,43 @@ __global__ __launch_bounds__(NT) void smp_main(SmpArgs A) {
   }
 
   // ---- 4. finish ----------------------------------------------------------
-  uint64_t rmax = 0;
+  // One parallel pass over the segment records (their counts go to LDS,
+  // borrowing the weight area, which is not in use yet).
+  uint32_t* s_cnt = (uint32_t*)fl.w;         // [MAX_SEGMENTS]
+  uint32_t* s_off = s_cnt + MAX_SEGMENTS;    // [MAX_SEGMENTS]
+  uint64_t rmax = 0, rkb = 0;
   uint32_t rflags = 0;
-  int csum = 0;
   for (int s = tid; s < S; s += NT) {
     const SegInfo si = A.seg_info[(int64_t)row * S + s];
     rmax = si.maxp > rmax ? si.maxp : rmax;
+    rkb = si.th1 > rkb ? si.th1 : rkb;
     rflags |= si.flags;
-    csum += (int)si.count;
+    s_cnt[s] = si.count;
   }
   rmax = block_max_u64(rmax, red_u64);
-  csum = block_sum_int(csum, red_int);
+  rkb = block_max_u64(rkb, red_u64);
   {
-    // OR of flags through the int reduction slots
-    __syncthreads();
+    // OR of the segment flags across the block: every decision below
+    // (status, dense or compact) must be uniform over the block's threads
     uint32_t f = rflags;
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) f |= __shfl_xor(f, o);
+    __syncthreads();
     if (lane == 0) red_u32[wave] = f;
     __syncthreads();
     f = 0;
 #pragma unroll
     for (int w = 0; w < NW; ++w) f |= red_u32[w];
     rflags = f;
+  }
+  int csum;
+  {
+    // exclusive scan of the counts; thread t owns segments 2t and 2t+1
+    const int s0 = 2 * tid, s1 = 2 * tid + 1;
+    const int c0 = s0 < S ? (int)s_cnt[s0] : 0, c1 = s1 < S ? (int)s_cnt[s1] : 0;
+    const int ex = block_excl_scan(c0 + c1, red_int, &csum);
+    if (s0 < S) s_off[s0] = (uint32_t)ex;
+    if (s1 < S) s_off[s1] = (uint32_t)(ex + c0);
   }
   const float M = key2f(pk_key(rmax));
   double logZ = 0.0, rmass = 0.0;
@@ -753,19 +815,50 @@ __global__ __launch_bounds__(NT) void smp_main(SmpArgs A) {
   else if (rflags & F_NONFINITE) status = ST_ENONFINITE;
 
   if (status == ST_OK) {
-    const bool dense = A.force_dense || (rflags & F_OVERFLOW) || csum > CAP;
+    // Final threshold from exact row quantities: every block filtered with
+    // bounds no larger than these, so the survivors below are exactly the
+    // row's elements with key >= theta_f, whatever the rendezvous timing.
+    uint32_t theta_f = (uint32_t)rkb;
+    if (plan.need_rel) {
+      const uint32_t tr = relevance_key(M, P.temperature);
+      theta_f = tr < theta_f ? tr : theta_f;
+    }
+    if (theta_f < 1u) theta_f = 1u;
+    bool dense = A.force_dense || (rflags & F_OVERFLOW);
     const uint64_t* cand;
     double* wbuf;
-    int64_t ncand;
+    int64_t ncand = 0;
     if (!dense) {
-      // gather the survivors of every segment
-      int base = 0;
-      for (int s = 0; s < S; ++s) {
-        const int cs = (int)A.seg_info[(int64_t)row * S + s].count;
-        const uint64_t* src = A.seg_cand + ((int64_t)row * S + s) * CAPSEG;
-        for (int i = tid; i < cs; i += NT) fl.cand[base + i] = src[i];
-        base += cs;
+      // gather the survivors of every segment in one flat parallel pass
+      // (order is irrelevant: sorted next)
+      if (tid == 0) bc[6] = 0u;
+      __syncthreads();
+      const int64_t cbase = (int64_t)row * S * CAPSEG;
+      for (int i0 = 0; i0 < csum; i0 += NT) {
+        const int idx = i0 + tid;
+        bool keep = false;
+        uint64_t p = 0;
+        if (idx < csum) {
+          int lo = 0, hi = S - 1;  // largest s with s_off[s] <= idx
+          while (lo < hi) {
+            const int mid = (lo + hi + 1) >> 1;
+            if ((int)s_off[mid] <= idx) lo = mid; else hi = mid - 1;
+          }
+          p = A.seg_cand[cbase + (int64_t)lo * CAPSEG + (idx - (int)s_off[lo])];
+          keep = pk_key(p) >= theta_f;
+        }
+        const uint64_t m = __ballot(keep);
+        uint32_t base = 0;
+        if (lane == 0 && m) base = atomicAdd(&bc[6], (uint32_t)__popcll(m));
+        base = __shfl(base, 0);
+        const uint32_t slot = base + (uint32_t)__popcll(m & ((lane == 0) ? 0ull : (~0ull >> (64 - lane))));
+        if (keep && slot < (uint32_t)CAP) fl.cand[slot] = p;
       }
+      __syncthreads();
+      csum = (int)bc[6];
+      if (csum > CAP || csum < 1) dense = true;
+    }
+    if (!dense) {
       int n2 = 1;
       while (n2 < csum) n2 <<= 1;
       for (int i = csum + tid; i < n2; i += NT) fl.cand[i] = 0ull;
@@ -885,13 +978,13 @@ __global__ __launch_bounds__(NT) void smp_main(SmpArgs A) {
 
   // ---- verify: the last finished row applies the acceptance rule --------
   if (A.mode == MODE_VERIFY) {
-    __threadfence();
     __syncthreads();
     if (tid == 0) {
-      const uint32_t old = __hip_atomic_fetch_add(A.vcount, 1u, __ATOMIC_ACQ_REL,
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+      const uint32_t old = __hip_atomic_fetch_add(A.vcount, 1u, __ATOMIC_RELAXED,
                                                   __HIP_MEMORY_SCOPE_AGENT);
       if (old == (uint32_t)(A.rows - 1)) {
-        __threadfence();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
         uint32_t emitted = 0, accepted = 0, token = 0xffffffffu;
         int32_t stop_eos = 0;
         bool ok = true;
@@ -1012,7 +1105,7 @@ __global__ __launch_bounds__(1024) void smp_penalty_prep(PenArgs A) {
 // ---------------------------------------------------------------------------
 template <int DT, bool VEC, bool PEN>
 static hipError_t launch_t(const SmpArgs& a, hipStream_t st) {
-  hipLaunchKernelGGL((smp_main<DT, VEC, PEN>), dim3(a.S, a.rows), dim3(NT), 0, st, a);
+  hipLaunchKernelGGL((smp_main<DT, VEC, PEN>), dim3((unsigned)(a.S * a.rows)), dim3(NT), 0, st, a);
   return hipGetLastError();
 }
 

@@ -91,7 +91,7 @@ EXPORTED = [
     "yskn_smp_last_error", "yskn_smp_create", "yskn_smp_destroy", "yskn_smp_set_params",
     "yskn_smp_sample", "yskn_smp_argmax", "yskn_smp_top_tokens", "yskn_smp_nll",
     "yskn_smp_verify", "yskn_smp_sync", "yskn_smp_select_host", "yskn_smp_validate_params",
-    "yskn_smp_version",
+    "yskn_smp_version", "yskn_smp_get_stats",
 ]
 
 _lib = None
@@ -120,6 +120,8 @@ def load_library(path: str = LIB_PATH) -> C.CDLL:
     L.yskn_smp_sync.argtypes = [vp, vp]
     L.yskn_smp_select_host.argtypes = [vp, vp, i32, u64, C.POINTER(u32)]
     L.yskn_smp_validate_params.argtypes = [C.POINTER(CParams), i32, u32]
+    L.yskn_smp_get_stats.argtypes = [vp, C.POINTER(C.c_uint64), i32]
+    L.yskn_smp_get_stats.restype = C.c_int
     for name in ("yskn_smp_create", "yskn_smp_set_params", "yskn_smp_sample", "yskn_smp_argmax",
                  "yskn_smp_top_tokens", "yskn_smp_nll", "yskn_smp_verify", "yskn_smp_sync",
                  "yskn_smp_select_host", "yskn_smp_validate_params"):
@@ -336,6 +338,16 @@ class DeviceSampler:
 
     def sync(self) -> None:
         _raise(self.L.yskn_smp_sync(self.h, self._stream()))
+
+    STAT_NAMES = ("rows", "dense_rows", "wait_timeouts", "candidates", "spins")
+
+    def stats(self) -> dict:
+        """Cumulative profiling counters of the handle (synchronises)."""
+        buf = (C.c_uint64 * len(self.STAT_NAMES))()
+        n = self.L.yskn_smp_get_stats(self.h, buf, len(self.STAT_NAMES))
+        if n < 0:
+            _raise(n)
+        return {k: int(buf[i]) for i, k in enumerate(self.STAT_NAMES[:n])}
 
     def select(self, logits: np.ndarray, prediction_position: int) -> int:
         """Selector::select on a host slice (speculation.rs:121-131)."""
