@@ -33,7 +33,7 @@ extern "C" {
 #define YSKN_SMP_OK 0
 #define YSKN_SMP_EINVAL (-1)     /* Error::InvalidInput */
 #define YSKN_SMP_ENONFINITE (-2) /* Error::NonFinite("logits") */
-#define YSKN_SMP_ERANGE (-3)     /* vocabulary or rows beyond the handle's limits */
+#define YSKN_SMP_ERANGE (-3)     /* vocabulary (max 4,194,304) or rows beyond the handle's limits */
 #define YSKN_SMP_EDEVICE (-4)    /* HIP runtime failure */
 
 /* ---- handle flags ------------------------------------------------------- */
@@ -195,9 +195,9 @@ int yskn_smp_select_host(yskn_smp_handle h, const float* host_logits, int32_t vo
 
 /* Profiling counters of the handle, cumulative since create (no counterpart
  * in the reference, which has no sampler-level instrumentation): out[0] rows
- * finished, out[1] rows served by the exact large-candidate path, out[2] rows
- * whose segment rendezvous timed out, out[3] candidates handed to row
- * finishers, out[4] rendezvous polling iterations. Synchronises the device.
+ * finished, out[1] rows served by the exact large-candidate path, out[2]
+ * 2,048-logit wave segments the row finishers had to read a second time,
+ * out[3] survivors sorted by the row finishers. Synchronises the device.
  * Returns the number of counters written (<= n) or a negative status. */
 int yskn_smp_get_stats(yskn_smp_handle h, uint64_t* out, int32_t n);
 

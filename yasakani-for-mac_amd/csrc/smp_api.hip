@@ -32,8 +32,6 @@ int hip_fail(hipError_t e, const char* what) {
   return YSKN_SMP_EDEVICE;
 }
 
-constexpr int SPIN_LIMIT = 4096;
-
 }  // namespace
 
 struct yskn_smp {
@@ -45,9 +43,10 @@ struct yskn_smp {
   std::vector<yskn_smp_params> params;  // host copy, 1 or max_rows entries
   bool params_shared = true;
   DevParams* d_params = nullptr;
-  uint64_t* d_seg_cand = nullptr;
-  SegInfo* d_seg_info = nullptr;
-  RowSync* d_sync = nullptr;
+  uint64_t* d_wave_cand = nullptr;
+  WaveRec* d_wave_rec = nullptr;
+  uint64_t* d_slots = nullptr;
+  uint32_t* d_tops = nullptr;
   int32_t* d_status = nullptr;
   uint32_t* d_vcount = nullptr;
   uint32_t* d_vresult = nullptr;
@@ -66,7 +65,6 @@ struct yskn_smp {
   uint64_t* d_host_pos = nullptr;
   uint32_t* d_host_out = nullptr;
   int32_t last_rows = 0;
-  int32_t spin_limit = SPIN_LIMIT;
 };
 
 namespace {
@@ -192,15 +190,15 @@ SmpArgs base_args(yskn_smp_handle h, const void* logits, int32_t rows, int32_t v
   a.pen_ids = h->d_pen_ids;
   a.pen_cnt = h->d_pen_cnt;
   a.pen_len = h->d_pen_len;
-  a.seg_cand = h->d_seg_cand;
-  a.seg_info = h->d_seg_info;
-  a.sync = h->d_sync;
+  a.wave_cand = h->d_wave_cand;
+  a.wave_rec = h->d_wave_rec;
+  a.slots = h->d_slots;
+  a.tops = h->d_tops;
   a.dense_a = h->d_dense_a;
   a.dense_b = h->d_dense_b;
   a.dense_w = h->d_dense_w;
   a.dense_ld = h->dense_ld;
   a.force_dense = (h->flags & YSKN_SMP_FLAG_FORCE_DENSE) ? 1 : 0;
-  a.spin_limit = h->spin_limit;
   a.stats = h->d_stats;
   return a;
 }
@@ -230,8 +228,8 @@ int launch(yskn_smp_handle h, SmpArgs& a, int32_t dtype, bool pen, const yskn_sm
     hipError_t e = launch_penalty_prep(p, st);
     if (e != hipSuccess) return hip_fail(e, "penalty preparation launch");
   }
-  hipError_t e = launch_sample(a, dtype == YSKN_SMP_F32 ? 0 : 1, vector_ok(a.logits, dtype, a.ld),
-                               pen, st);
+  a.vec = vector_ok(a.logits, dtype, a.ld) ? 1 : 0;
+  hipError_t e = launch_sample(a, dtype == YSKN_SMP_F32 ? 0 : 1, a.vec != 0, pen, st);
   if (e != hipSuccess) return hip_fail(e, "sampler launch");
   h->last_rows = a.rows;
   return YSKN_SMP_OK;
@@ -257,7 +255,7 @@ int yskn_smp_create(int32_t max_rows, int32_t max_vocab, uint32_t flags, yskn_sm
   if (max_vocab <= 0)
     return fail(YSKN_SMP_EINVAL, "invalid input: logits must contain a nonempty u32-indexed vocabulary");
   if ((int64_t)max_vocab > (int64_t)SEG * MAX_SEGMENTS)
-    return fail(YSKN_SMP_ERANGE, "vocabulary larger than 16,777,216");
+    return fail(YSKN_SMP_ERANGE, "vocabulary larger than 4,194,304");
   yskn_smp* h = new yskn_smp();
   h->max_rows = max_rows;
   h->max_vocab = max_vocab;
@@ -265,9 +263,6 @@ int yskn_smp_create(int32_t max_rows, int32_t max_vocab, uint32_t flags, yskn_sm
   h->max_segments = (max_vocab + SEG - 1) / SEG;
   h->params.assign(1, default_params());
   h->params_shared = true;
-  // YSKN_SMP_SPIN_LIMIT bounds the rendezvous polling (0 disables waiting;
-  // results are identical, only the candidate filter is weaker).
-  if (const char* e = std::getenv("YSKN_SMP_SPIN_LIMIT")) h->spin_limit = std::atoi(e);
   if (hipGetDevice(&h->device) != hipSuccess) h->device = 0;
   const size_t R = (size_t)max_rows, Sg = (size_t)h->max_segments;
   h->dense_ld = ((int64_t)max_vocab + 63) / 64 * 64;
@@ -277,9 +272,10 @@ int yskn_smp_create(int32_t max_rows, int32_t max_vocab, uint32_t flags, yskn_sm
     if (e == hipSuccess) e = r;
   };
   step(alloc(&h->d_params, R));
-  step(alloc(&h->d_seg_cand, R * Sg * CAPSEG));
-  step(alloc(&h->d_seg_info, R * Sg));
-  step(alloc(&h->d_sync, R));
+  step(alloc(&h->d_wave_cand, R * Sg * NWS * WCAP));
+  step(alloc(&h->d_wave_rec, R * Sg * NWS));
+  step(alloc(&h->d_slots, R * (size_t)MAX_SEGMENTS));
+  step(alloc(&h->d_tops, R * (size_t)MAX_SEGMENTS * TOPS));
   step(alloc(&h->d_status, R));
   step(alloc(&h->d_vcount, 4));
   step(alloc(&h->d_vresult, 4));
@@ -294,7 +290,7 @@ int yskn_smp_create(int32_t max_rows, int32_t max_vocab, uint32_t flags, yskn_sm
   step(alloc(&h->d_host_logits, (size_t)max_vocab));
   step(alloc(&h->d_host_pos, 1));
   step(alloc(&h->d_host_out, 1));
-  if (e == hipSuccess) step(hipMemset(h->d_sync, 0, R * sizeof(RowSync)));
+  if (e == hipSuccess) step(hipMemset(h->d_slots, 0, R * (size_t)MAX_SEGMENTS * sizeof(uint64_t)));
   if (e == hipSuccess) step(hipMemset(h->d_status, 0, R * sizeof(int32_t)));
   if (e == hipSuccess) step(hipMemset(h->d_vcount, 0, 4 * sizeof(uint32_t)));
   if (e == hipSuccess) step(hipMemset(h->d_pen_len, 0, R * sizeof(int32_t)));
@@ -313,7 +309,7 @@ int yskn_smp_create(int32_t max_rows, int32_t max_vocab, uint32_t flags, yskn_sm
 
 void yskn_smp_destroy(yskn_smp_handle h) {
   if (!h) return;
-  void* ptrs[] = {h->d_params,     h->d_seg_cand,  h->d_seg_info,    h->d_sync,
+  void* ptrs[] = {h->d_params,     h->d_wave_cand, h->d_wave_rec,    h->d_slots,    h->d_tops,
                   h->d_status,     h->d_vcount,    h->d_vresult,     h->d_dense_a,
                   h->d_dense_b,    h->d_dense_w,   h->d_pen_bitmap,  h->d_pen_ids,
                   h->d_pen_cnt,    h->d_pen_len,   h->d_stats,       h->d_host_logits,

@@ -6,29 +6,38 @@
 
 namespace yskn {
 
-// Launch geometry. One block owns a 16,384-element segment of a row, held in
-// registers (32 elements per thread); a row of V logits spans S = ceil(V/SEG)
-// blocks.
-constexpr int NT = 512;            // threads per block (8 wave64s)
-constexpr int NW = NT / 64;        // waves per block
-constexpr int EPT = 32;            // elements per thread
-constexpr int SEG = NT * EPT;      // elements per block
-constexpr int CAPSEG = 2048;       // candidates a block may hand to its row's finisher
-constexpr int CAP = 2048;          // candidates the finisher sorts in LDS
+// Scan geometry. A scan block of 8 wave64s owns a 16,384-element segment of
+// a row; each wave owns 2,048 consecutive elements (32 per lane, coalesced
+// 16-byte loads), held in registers. A row of V logits spans S = ceil(V/SEG)
+// scan blocks and W = 8 * S wave records. The finisher uses 8 waves per row.
+constexpr int NTS = 512;           // threads per scan block (8 wave64s)
+constexpr int NWS = NTS / 64;      // waves per scan block
+constexpr int NT = 512;            // threads per finisher block (8 wave64s)
+constexpr int NW = NT / 64;        // waves per finisher block
+constexpr int EPT = 32;            // elements per lane
+constexpr int WSEG = 64 * EPT;     // elements per wave
+constexpr int SEG = NTS * EPT;     // elements per scan block
+constexpr int WCAP = 256;          // candidates a wave may hand to its row's finisher
+constexpr int CAP = 4096;          // candidates the finisher sorts in LDS
 constexpr int KBMAX = 64;          // largest "small" top-k / list length
 constexpr int HCAP = 16384;        // history tokens per row for the penalties
-constexpr int MAX_SEGMENTS = 1024; // V <= 16,777,216
+constexpr int MAX_SEGMENTS = 256;  // V <= 4,194,304
+constexpr int MAX_WAVES = MAX_SEGMENTS * NWS;
+constexpr uint32_t RESCAN = 0xffffffffu;  // wave record count: finisher re-scans the wave
+constexpr int TOPS = 8;            // lane maxima each scan block publishes (NWS * TOPS == 64)
+static_assert(NWS * TOPS == 64, "one wave merges the block's published lane maxima");
 
 // Binary64 log-domain cut for the serial-sum argument: a weight exp_d(z)
 // with z < -37.5 is below 2^-53 and cannot change a running binary64 sum
 // that is already >= 1.
 constexpr double ZCUT = -37.5;
+// Terms exp(l - m) with l < m - ZMASS are left out of the logprob mass: at
+// most V * e^-40 < 7e-11 relative for V <= 4,194,304.
+constexpr float ZMASS = 40.0f;
 
-// Segment flags.
+// Wave flags.
 constexpr uint32_t F_NONFINITE = 1u;
-constexpr uint32_t F_OVERFLOW = 2u;
 constexpr uint32_t F_INVALID = 4u;
-constexpr uint32_t F_TIMEOUT = 8u;
 
 // Status codes (public values of include/yskn_smp.h).
 constexpr int32_t ST_OK = 0;
@@ -49,31 +58,26 @@ struct DevParams {
   int32_t pad;
 };
 
-// What a segment block hands to the row's finisher.
-struct SegInfo {
-  uint64_t maxp;  // packed (key << 32) | ~id of the segment's largest logit
-  double mass;    // sum of exp(l - mref) over the segment (binary32 terms)
-  float mref;     // reference point of mass
-  uint32_t count; // candidates written (<= CAPSEG)
-  uint32_t flags; // F_*
-  uint32_t th1;   // the block's top-KB threshold key
+// What a wave hands to its row's finisher (32 bytes).
+struct WaveRec {
+  uint64_t maxp;   // packed (key << 32) | ~id of the wave's largest logit (0: no elements)
+  double mass;     // sum of exp(l - mref) over the wave's elements with l >= mref - ZMASS
+  float mref;      // reference point of mass
+  uint32_t count;  // candidates written (<= WCAP) or RESCAN
+  uint32_t th1;    // the block's top-KB threshold key
+  uint32_t flags;  // F_*
 };
 
-// Per-row rendezvous counters; all zero between launches.
-struct RowSync {
-  uint32_t arrive;    // blocks that published their maxima
-  uint32_t done;      // blocks that finished their segment
-  uint32_t hint_max;  // max over published segment max keys
-  uint32_t hint_kb;   // max over published top-KB thresholds
-};
+// Per-block bound slots: slot (row, seg) holds (top-KB threshold key << 32 |
+// block max key) once the block has published it, 0 otherwise. Zero between
+// calls (the finisher clears its row).
 
 // Counters for profiling the path (cumulative since create).
 enum StatIndex {
-  STAT_ROWS = 0,       // rows finished
-  STAT_DENSE_ROWS,     // rows served by the exact large-candidate path
-  STAT_WAIT_TIMEOUTS,  // segment blocks whose rendezvous timed out
-  STAT_CANDIDATES,     // candidates handed to finishers
-  STAT_SPINS,          // rendezvous polling iterations over all blocks
+  STAT_ROWS = 0,      // rows finished
+  STAT_DENSE_ROWS,    // rows served by the exact large-candidate path
+  STAT_RESCAN_WAVES,  // wave segments the finishers re-read
+  STAT_CANDIDATES,    // survivors sorted by finishers
   STAT_COUNT
 };
 
@@ -84,7 +88,7 @@ struct SmpArgs {
   int64_t ld;  // elements between rows
   int32_t V;
   int32_t rows;
-  int32_t S;
+  int32_t S;   // scan blocks per row
   int32_t mode;
   const DevParams* prm;
   int32_t prm_shared;
@@ -115,15 +119,16 @@ struct SmpArgs {
   const uint32_t* pen_cnt;     // [rows][HCAP]
   const int32_t* pen_len;      // [rows], -1 = invalid history
   // workspace
-  uint64_t* seg_cand;  // [rows][S][CAPSEG]
-  SegInfo* seg_info;   // [rows][S]
-  RowSync* sync;       // [rows]
-  uint64_t* dense_a;   // [rows][dense_ld]
+  uint64_t* wave_cand;  // [rows][S * NWS][WCAP]
+  WaveRec* wave_rec;    // [rows][S * NWS]
+  uint64_t* slots;      // [rows][MAX_SEGMENTS]
+  uint32_t* tops;       // [rows][MAX_SEGMENTS][TOPS] each block's largest lane maxima
+  uint64_t* dense_a;    // [rows][dense_ld]
   uint64_t* dense_b;
   double* dense_w;
   int64_t dense_ld;
   int32_t force_dense;
-  int32_t spin_limit;
+  int32_t vec;          // rows are 16-byte aligned with ld a multiple of 16 bytes
   unsigned long long* stats;
   // verify
   const uint32_t* drafts;

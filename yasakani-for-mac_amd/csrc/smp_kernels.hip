@@ -1,24 +1,29 @@
 // smp_kernels.hip -- gfx950 kernels of the per-step sampling path.
 //
-// One launch per call. S * rows blocks: block (seg, row) owns 16,384 logits of
-// the row in registers (32 per thread, coalesced 16-byte loads). The path:
+// Two launches per call (three with penalties):
 //
-//  1. scan: order-preserving 32-bit keys, segment max, non-finite check.
-//  2. row bounds: each block publishes its max key and a top-KB threshold
-//     with agent-scope atomic max operations, whose return values give it
-//     the row's running maxima at once. A block that would keep too many
-//     elements under those bounds waits, with a bounded spin that always
-//     ends, until every block of its row has published.
-//  3. filter: a block keeps only elements that can matter to the reference
-//     algorithm: (a) elements whose binary64 weight exp_d((l - M)/T) can
-//     reach 2^-53 -- smaller weights are absorbed by the reference's serial
-//     binary64 sums, whose running value is >= 1 -- and (b) a superset of the
-//     row's top-KB by value. Survivors are written compactly for the row.
-//  4. finish: the last block of the row gathers the survivors, sorts them in
-//     LDS by (value desc, id asc) and runs the reference's serial binary64
-//     truncation and draw on them (output_head_sampler.rs:136-212).
-//     Rows with more survivors than LDS holds take the exact "dense" path:
-//     radix select, stable LSD radix sort in global scratch, same tail.
+//  smp_scan   S * rows blocks of 8 wave64s. Each wave owns 2,048 consecutive
+//             logits of a row in registers (32 per lane, coalesced 16-byte
+//             loads) and works on them without waiting for anyone:
+//             order-preserving 32-bit keys, wave max, a top-KB threshold,
+//             one block barrier to share both, then per wave an agent-scope
+//             atomic max that returns the row's running bounds. With them
+//             the wave keeps only elements that can matter to the reference
+//             algorithm -- (a) elements whose binary64 weight
+//             exp_d((l - M)/T) can reach 2^-53 (smaller weights are absorbed
+//             by the reference's serial binary64 sums, whose running value is
+//             >= 1) and (b) a superset of the row's top-KB by value -- and
+//             hands them to its row's finisher. A wave that would hand over
+//             more than WCAP elements hands over none and is re-read by the
+//             finisher instead.
+//  smp_finish one block per row. Exact row maximum and top-KB threshold from
+//             the wave records give the final threshold; the survivors (which
+//             do not depend on timing) are sorted in LDS by (value desc,
+//             id asc) and the reference's serial binary64 truncation and
+//             draw run on them (output_head_sampler.rs:136-212). Rows with
+//             more survivors than LDS holds take the exact "dense" path:
+//             radix select, stable LSD radix sort in global scratch, same
+//             tail.
 //
 // Ordering is (value desc, id asc) everywhere, as output_head_sampler.rs:
 // 124-132; -0 and +0 compare equal (keys canonicalise -0 to +0) and ties go
@@ -63,6 +68,14 @@ __device__ __forceinline__ uint32_t relevance_key(float M, double T) {
   return k < 1u ? 1u : k;
 }
 
+// The binary32 value t with {v : v >= t} == {v : f2key(v) >= theta} over
+// finite values: key thresholds at or below the key of -FLT_MAX keep every
+// finite value; 0xffffffff (a NaN pattern) keeps none.
+__device__ __forceinline__ float key_threshold_float(uint32_t theta) {
+  if (theta <= 0x00800000u) return -3.4028234663852886e38f;
+  return key2f(theta);
+}
+
 // ---------------------------------------------------------------------------
 // wave64 / block reductions
 // ---------------------------------------------------------------------------
@@ -70,6 +83,14 @@ __device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) {
     const uint64_t w = __shfl_xor(v, o);
+    v = v > w ? v : w;
+  }
+  return v;
+}
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    const uint32_t w = __shfl_xor(v, o);
     v = v > w ? v : w;
   }
   return v;
@@ -99,6 +120,54 @@ __device__ __forceinline__ int wave_incl_scan(int x, int lane) {
     if (lane >= o) x += y;
   }
   return x;
+}
+
+// k-th largest (1 <= k <= 64) of one value per lane: bitonic sort of the
+// 64 lane values (ascending) through cross-lane shuffles, then lane 64 - k.
+__device__ __forceinline__ uint32_t wave_kth_largest(uint32_t v, int k) {
+  const int lane = threadIdx.x & 63;
+#pragma unroll
+  for (int size = 2; size <= 64; size <<= 1) {
+#pragma unroll
+    for (int j = size >> 1; j > 0; j >>= 1) {
+      const uint32_t o = __shfl_xor(v, j);
+      const bool take_min = ((lane & size) == 0) == ((lane & j) == 0);
+      v = take_min ? (v < o ? v : o) : (v > o ? v : o);
+    }
+  }
+  return __shfl(v, 64 - k);
+}
+
+// Ascending bitonic sort of one value per lane across the wave: lane i
+// returns the i-th smallest.
+__device__ __forceinline__ uint32_t wave_sort_asc(uint32_t v) {
+  const int lane = threadIdx.x & 63;
+#pragma unroll
+  for (int size = 2; size <= 64; size <<= 1) {
+#pragma unroll
+    for (int j = size >> 1; j > 0; j >>= 1) {
+      const uint32_t o = __shfl_xor(v, j);
+      const bool take_min = ((lane & size) == 0) == ((lane & j) == 0);
+      v = take_min ? (v < o ? v : o) : (v > o ? v : o);
+    }
+  }
+  return v;
+}
+
+// The ka-th and kb-th largest (1 <= ka, kb <= 64) of one value per lane.
+__device__ __forceinline__ void wave_kth_pair(uint32_t v, int ka, int kb, uint32_t* a, uint32_t* b) {
+  const int lane = threadIdx.x & 63;
+#pragma unroll
+  for (int size = 2; size <= 64; size <<= 1) {
+#pragma unroll
+    for (int j = size >> 1; j > 0; j >>= 1) {
+      const uint32_t o = __shfl_xor(v, j);
+      const bool take_min = ((lane & size) == 0) == ((lane & j) == 0);
+      v = take_min ? (v < o ? v : o) : (v > o ? v : o);
+    }
+  }
+  *a = __shfl(v, 64 - ka);
+  *b = __shfl(v, 64 - kb);
 }
 
 // Block-wide reductions through a small LDS array (NW entries). Every
@@ -234,11 +303,14 @@ __device__ __forceinline__ uint64_t position_of(const SmpArgs& A, int row, int d
 }
 
 // ---------------------------------------------------------------------------
-// LDS layout of the finisher (32 KB), reused by the dense path.
+// LDS layout of the finisher (88 KB); the dense path borrows `cand`.
 // ---------------------------------------------------------------------------
 struct FinishLds {
-  uint64_t cand[CAP];  // sorted candidates (LDS path)
-  double w[CAP];       // weights of the first c candidates (LDS path)
+  uint64_t cand[CAP];          // survivors, sorted (compact path)
+  double w[CAP];               // weights of the first c candidates (compact path)
+  uint32_t cnt[MAX_WAVES];     // per wave: candidates handed over (0 if re-scanned)
+  uint32_t off[MAX_WAVES];     // exclusive prefix of cnt
+  uint32_t res[MAX_WAVES];     // indices of the waves to re-scan
 };
 
 // ---------------------------------------------------------------------------
@@ -497,24 +569,65 @@ __device__ int64_t dense_build(const SmpArgs& A, const RowCtx& rc, int row, uint
 }
 
 // ---------------------------------------------------------------------------
-// The fused kernel.
+// Shared per-row set-up of both kernels.
+// ---------------------------------------------------------------------------
+template <bool PEN>
+__device__ __forceinline__ RowCtx make_rowctx(const SmpArgs& A, const DevParams& P, int row,
+                                              int dtype_bytes, uint32_t* flags) {
+  RowCtx rc;
+  rc.base = (const char*)A.logits + (int64_t)row * A.ld * dtype_bytes;
+  rc.bitmap = nullptr;
+  rc.pids = nullptr;
+  rc.pcnt = nullptr;
+  rc.plen = 0;
+  rc.rep = P.rep;
+  rc.pres = P.pres;
+  rc.freq = P.freq;
+  if (PEN && P.penalize) {
+    rc.plen = A.pen_len[row];
+    if (rc.plen < 0) {
+      *flags |= F_INVALID;
+      rc.plen = 0;
+    } else {
+      rc.bitmap = A.pen_bitmap + (int64_t)row * A.bm_ld;
+      rc.pids = A.pen_ids + (int64_t)row * HCAP;
+      rc.pcnt = A.pen_cnt + (int64_t)row * HCAP;
+    }
+  }
+  return rc;
+}
+
+// Order-preserving final threshold of a row: a block or wave with bounds
+// (m, kb) keeps key >= threshold(m, kb); the threshold never decreases as
+// the bounds grow, so bounds seen early give supersets of the final set.
+__device__ __forceinline__ uint32_t row_threshold(const RowPlan& plan, const DevParams& P,
+                                                  float m, uint32_t kb) {
+  uint32_t t = kb;
+  if (plan.need_rel) {
+    const uint32_t tr = relevance_key(m, P.temperature);
+    t = tr < t ? tr : t;
+  }
+  return t < 1u ? 1u : t;
+}
+
+// ---------------------------------------------------------------------------
+// smp_scan: one wave per 2,048 logits.
 // ---------------------------------------------------------------------------
 template <int DT, bool VEC, bool PEN>
-__global__ __launch_bounds__(NT) void smp_main(SmpArgs A) {
-  __shared__ FinishLds fl;
-  __shared__ uint64_t red_u64[NW];
-  __shared__ double red_f64[NW];
-  __shared__ int red_int[NW];
-  __shared__ uint32_t red_u32[NW];
-  __shared__ uint32_t bc[8];
-  __shared__ TailShared ts;
+__global__ __launch_bounds__(NTS) __attribute__((amdgpu_waves_per_eu(6))) void smp_scan(SmpArgs A) {
+  __shared__ uint64_t s_wmax[NWS];
+  __shared__ uint32_t s_wtb[NWS];
+  __shared__ uint32_t s_top[NWS * TOPS];
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  // wave index and every per-wave quantity below are uniform: keep them in
+  // scalar registers (readfirstlane) so the 32 keys own the vector file
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int S = A.S;
+  const int32_t V = A.V;
   // Workgroups are dealt round-robin to the 8 XCDs (linear id mod 8). Groups
-  // of 8 rows are laid out so that all S segments of a row share one XCD:
-  // its segments are dispatched together by one dispatcher and the row's
-  // hand-off traffic stays within one L2.
+  // of 8 rows are laid out so that all S blocks of a row share one XCD: they
+  // are dispatched together by one dispatcher and their bounds arrive early.
   int row, seg;
   {
     const int b = blockIdx.x;
@@ -529,256 +642,383 @@ __global__ __launch_bounds__(NT) void smp_main(SmpArgs A) {
       seg = r - (r / S) * S;
     }
   }
-  const int32_t V = A.V;
   const DevParams P = A.prm[A.prm_shared ? 0 : row];
   const RowPlan plan = make_plan(A, P);
+  uint32_t wflags = 0;
+  const RowCtx rc = make_rowctx<PEN>(A, P, row, DT == 0 ? 4 : 2, &wflags);
 
-  RowCtx rc;
-  rc.base = (const char*)A.logits + (int64_t)row * A.ld * (DT == 0 ? 4 : 2);
-  rc.bitmap = nullptr;
-  rc.pids = nullptr;
-  rc.pcnt = nullptr;
-  rc.plen = 0;
-  rc.rep = P.rep;
-  rc.pres = P.pres;
-  rc.freq = P.freq;
-  uint32_t seg_flags = 0;
-  if (PEN && P.penalize) {
-    rc.plen = A.pen_len[row];
-    if (rc.plen < 0) {
-      seg_flags |= F_INVALID;
-      rc.plen = 0;
-    } else {
-      rc.bitmap = A.pen_bitmap + (int64_t)row * A.bm_ld;
-      rc.pids = A.pen_ids + (int64_t)row * HCAP;
-      rc.pcnt = A.pen_cnt + (int64_t)row * HCAP;
-    }
-  }
-
-  // ---- 1. load the segment into registers as keys -----------------------
-  const int64_t seg0 = (int64_t)seg * SEG;
-  uint32_t key[EPT];
+  // ---- load 32 logits per lane as raw bits ------------------------------
+  // Element of (q, c) for this lane: e = ebase + q * 64 * GRP + c (32-bit:
+  // V <= 4,194,304). A wave whose 2,048 elements are all inside the row
+  // (every wave but the row's last) runs without per-element bounds checks.
   constexpr int GRP = (DT == 0) ? 4 : 8;  // elements per 16-byte load
   constexpr int NGRP = EPT / GRP;
+  const uint32_t w0 = (uint32_t)seg * SEG + (uint32_t)wave * WSEG;
+  const uint32_t ebase = w0 + (uint32_t)lane * GRP;
+  const bool full = w0 + WSEG <= (uint32_t)V;
+  uint32_t key[EPT];
+  if (VEC && full) {
+    const uint4* src = (const uint4*)(rc.base + (size_t)ebase * (DT == 0 ? 4 : 2));
 #pragma unroll
-  for (int q = 0; q < NGRP; ++q) {
-    const int64_t e0 = seg0 + (int64_t)(q * NT + tid) * GRP;
-    if (VEC && e0 + GRP <= V) {
-      const uint4 v = *(const uint4*)(rc.base + e0 * (DT == 0 ? 4 : 2));
+    for (int q = 0; q < NGRP; ++q) {
+      const uint4 v = src[q * 64];
       if (DT == 0) {
         key[q * 4 + 0] = v.x;
         key[q * 4 + 1] = v.y;
         key[q * 4 + 2] = v.z;
         key[q * 4 + 3] = v.w;
       } else {
-        const uint32_t wv[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-        for (int c = 0; c < 4; ++c) {
-          key[q * 8 + 2 * c] = wv[c] << 16;
-          key[q * 8 + 2 * c + 1] = wv[c] & 0xffff0000u;
-        }
-      }
-    } else {
-#pragma unroll
-      for (int c = 0; c < GRP; ++c) key[q * GRP + c] = (e0 + c < V) ? raw_bits<DT>(rc, e0 + c) : 0u;
-    }
-  }
-  bool bad = false;
-  uint64_t tmax = 0;
-#pragma unroll
-  for (int q = 0; q < NGRP; ++q) {
-    const int64_t e0 = seg0 + (int64_t)(q * NT + tid) * GRP;
-    uint32_t wbits = 0;
-    if (PEN && rc.bitmap && e0 < V) wbits = rc.bitmap[e0 >> 5];
-#pragma unroll
-    for (int c = 0; c < GRP; ++c) {
-      const int64_t e = e0 + c;
-      uint32_t b = key[q * GRP + c];
-      if (e < V) {
-        if (PEN && rc.bitmap && ((wbits >> (e & 31)) & 1u)) b = penalize(b, pen_count(rc, (uint32_t)e), rc);
-        bad |= nonfinite_bits(b);
-        const uint32_t k = f2key(b);
-        key[q * GRP + c] = k;
-        const uint64_t p = pack(k, (uint32_t)e);
-        tmax = p > tmax ? p : tmax;
-      } else {
-        key[q * GRP + c] = 0u;
+        key[q * 8 + 0] = v.x << 16;
+        key[q * 8 + 1] = v.x & 0xffff0000u;
+        key[q * 8 + 2] = v.y << 16;
+        key[q * 8 + 3] = v.y & 0xffff0000u;
+        key[q * 8 + 4] = v.z << 16;
+        key[q * 8 + 5] = v.z & 0xffff0000u;
+        key[q * 8 + 6] = v.w << 16;
+        key[q * 8 + 7] = v.w & 0xffff0000u;
       }
     }
-  }
-  if (__syncthreads_or(bad)) seg_flags |= F_NONFINITE;
-  const uint64_t bmax = block_max_u64(tmax, red_u64);
-  const uint32_t key_b = pk_key(bmax);
-
-  // ---- top-KB threshold: per wave the ceil(KB/8)-th largest thread max;
-  // at least KB elements of the segment lie at or above the minimum over waves.
-  {
-    const int qp = (plan.KB + NW - 1) / NW;
-    uint64_t mine = tmax, last = 0;
-    for (int i = 0; i < qp; ++i) {
-      const uint64_t m = wave_max_u64(mine);
-      last = m;
-      if (mine == m) mine = 0;
-    }
-    __syncthreads();
-    if (lane == 0) red_u32[wave] = pk_key(last);
-    __syncthreads();
-  }
-  uint32_t th1 = red_u32[0];
-#pragma unroll
-  for (int w = 1; w < NW; ++w) th1 = th1 < red_u32[w] ? th1 : red_u32[w];
-
-  // ---- 2. row bounds -------------------------------------------------------
-  // Each block publishes its max key and its top-KB threshold; fetch_max
-  // returns the row's running maxima, so a block obtains bounds without
-  // waiting. Only monotone bounds travel this way: any value read is a valid
-  // (if weaker) bound, so relaxed atomics suffice and no cache-wide fence is
-  // issued while blocks stream their segments.
-  if (tid == 0) {
-    RowSync* rs = A.sync + row;
-    const uint32_t om = __hip_atomic_fetch_max(&rs->hint_max, key_b, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    const uint32_t ok = __hip_atomic_fetch_max(&rs->hint_kb, th1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    __hip_atomic_fetch_add(&rs->arrive, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    bc[0] = om > key_b ? om : key_b;
-    bc[1] = ok > th1 ? ok : th1;
-    bc[2] = 0u;
-  }
-  __syncthreads();
-  uint32_t mkey = bc[0];
-  uint32_t th_kb = bc[1];
-  float m_ref = key2f(mkey);
-
-  // ---- 3. filter --------------------------------------------------------
-  auto threshold = [&](float mr, uint32_t kb) {
-    uint32_t t = kb;
-    if (plan.need_rel) {
-      const uint32_t tr = relevance_key(mr, P.temperature);
-      t = tr < t ? tr : t;
-    }
-    if (A.force_dense) t = 0xffffffffu;  // compact path unused
-    return t < 1u ? 1u : t;
-  };
-  uint32_t theta = threshold(m_ref, th_kb);
-  int cnt = 0;
-#pragma unroll
-  for (int i = 0; i < EPT; ++i) cnt += (key[i] >= theta) ? 1 : 0;
-  int total = block_sum_int(cnt, red_int);
-  if (total > CAPSEG / 2 && A.spin_limit > 0) {
-    // Too many survivors under the bounds seen so far: wait (bounded) until
-    // every block of the row has published, then filter again.
-    if (tid == 0) {
-      RowSync* rs = A.sync + row;
-      uint32_t n = 0;
-      int it = 0;
-      for (; it < A.spin_limit; ++it) {
-        n = __hip_atomic_load(&rs->arrive, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        if (n >= (uint32_t)S) break;
-        __builtin_amdgcn_s_sleep(2);
-      }
-      if (A.stats) atomicAdd(&A.stats[STAT_SPINS], (unsigned long long)it + 1ull);
-      const uint32_t hm = __hip_atomic_load(&rs->hint_max, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      const uint32_t hk = __hip_atomic_load(&rs->hint_kb, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      bc[3] = hm > mkey ? hm : mkey;
-      bc[4] = hk > th_kb ? hk : th_kb;
-      bc[2] = n >= (uint32_t)S ? 0u : F_TIMEOUT;
-    }
-    __syncthreads();
-    mkey = bc[3];
-    th_kb = bc[4];
-    m_ref = key2f(mkey);
-    theta = threshold(m_ref, th_kb);
-    cnt = 0;
-#pragma unroll
-    for (int i = 0; i < EPT; ++i) cnt += (key[i] >= theta) ? 1 : 0;
-  }
-  seg_flags |= bc[2];
-
-  // mass relative to m_ref: binary32 terms, pairwise within the thread
-  double mass = 0.0;
-  if (A.want_mass) {
-    float acc[EPT];
-#pragma unroll
-    for (int i = 0; i < EPT; ++i) {
-      const uint32_t k = key[i];
-      const float x = k ? (key2f(k) - m_ref) : -__builtin_inff();
-      acc[i] = __builtin_amdgcn_exp2f(x * 1.4426950408889634f);
-    }
-#pragma unroll
-    for (int s = EPT / 2; s > 0; s >>= 1) {
-#pragma unroll
-      for (int i = 0; i < s; ++i) acc[i] = acc[i] + acc[i + s];
-    }
-    mass = block_sum_f64((double)acc[0], red_f64);
-  }
-
-  const int off = block_excl_scan(cnt, red_int, &total);
-  const bool overflow = total > CAPSEG;
-  if (!overflow && cnt) {
-    uint64_t* dst = A.seg_cand + ((int64_t)row * S + seg) * CAPSEG + off;
-    int o = 0;
+  } else {
 #pragma unroll
     for (int q = 0; q < NGRP; ++q) {
 #pragma unroll
       for (int c = 0; c < GRP; ++c) {
-        const uint32_t k = key[q * GRP + c];
-        if (k >= theta) {
-          const int64_t e = seg0 + (int64_t)(q * NT + tid) * GRP + c;
-          dst[o++] = pack(k, (uint32_t)e);
+        const uint32_t e = ebase + q * 64 * GRP + c;
+        key[q * GRP + c] = e < (uint32_t)V ? raw_bits<DT>(rc, e) : 0u;
+      }
+    }
+  }
+  // ---- values, lane max (first index on ties: indices grow with q, c) ---
+  // The hot loop works on binary32 values: IEEE comparisons treat -0 and +0
+  // as equal, exactly like the canonical keys; 32-bit keys are formed only
+  // for the lane maximum and for the elements handed over. Absent elements
+  // (past the row's end) are -inf, which no threshold keeps.
+  float val[EPT];
+  bool bad = false;
+  float lmax = -__builtin_inff();
+  uint32_t imax = 0;
+#pragma unroll
+  for (int q = 0; q < NGRP; ++q) {
+    uint32_t wbits = 0;
+    const uint32_t e0 = ebase + q * 64 * GRP;
+    if (PEN && rc.bitmap && e0 < (uint32_t)V) wbits = rc.bitmap[e0 >> 5];
+#pragma unroll
+    for (int c = 0; c < GRP; ++c) {
+      const uint32_t e = e0 + c;
+      uint32_t b = key[q * GRP + c];
+      float v = -__builtin_inff();
+      if (full || e < (uint32_t)V) {
+        if (PEN && rc.bitmap && ((wbits >> (e & 31)) & 1u)) b = penalize(b, pen_count(rc, e), rc);
+        v = __uint_as_float(b);
+        bad |= __builtin_amdgcn_class(v, 0x207) != 0;  // signaling/quiet NaN, +-inf
+      }
+      val[q * GRP + c] = v;
+      // track the offset (an immediate) rather than the index: no per-element
+      // index register stays live into the hand-over below
+      if (v > lmax) {
+        lmax = v;
+        imax = q * 64 * GRP + c;
+      }
+    }
+  }
+  imax += ebase;
+  if (__ballot(bad)) wflags |= F_NONFINITE;
+  const uint32_t kmax = lmax == -__builtin_inff() ? 0u : f2key(__float_as_uint(lmax));
+  const uint64_t wmax = wave_max_u64(kmax ? pack(kmax, imax) : 0ull);
+  // Top-KB threshold of the block: per wave the ceil(KB/8)-th largest lane
+  // maximum (0 where too few lanes hold data); the minimum over the block's
+  // 8 waves has at least 8 * ceil(KB/8) >= KB elements at or above it.
+  const uint32_t lsorted = wave_sort_asc(kmax);
+  const uint32_t wb = __shfl(lsorted, 64 - (plan.KB + NWS - 1) / NWS);
+  if (lane == 0) {
+    s_wmax[wave] = wmax;
+    s_wtb[wave] = wb;
+  }
+  if (lane >= 64 - TOPS) s_top[wave * TOPS + lane - (64 - TOPS)] = lsorted;
+  __syncthreads();
+  // The block publishes its TOPS largest lane maxima: distinct elements of
+  // the row, from which the finisher takes a row-wide top-KB bound.
+  if (wave == 0) {
+    const uint32_t t = wave_sort_asc(s_top[lane]);
+    if (lane >= 64 - TOPS)
+      A.tops[((int64_t)row * MAX_SEGMENTS + seg) * TOPS + lane - (64 - TOPS)] = t;
+  }
+  // lane w < 8 reads wave w's record; three shuffle steps reduce them (few
+  // registers live next to the 32 keys)
+  uint64_t bmax = lane < NWS ? s_wmax[lane] : 0ull;
+  uint32_t thb = lane < NWS ? s_wtb[lane] : 0xffffffffu;
+#pragma unroll
+  for (int o = NWS / 2; o > 0; o >>= 1) {
+    const uint64_t ob = __shfl_xor(bmax, o);
+    const uint32_t oc = __shfl_xor(thb, o);
+    bmax = ob > bmax ? ob : bmax;
+    thb = oc < thb ? oc : thb;
+  }
+  // (readfirstlane yields int: convert through uint32_t, never sign-extend)
+  bmax = ((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(bmax >> 32)) << 32) |
+         (uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)bmax);
+  const uint32_t th1 = (uint32_t)__builtin_amdgcn_readfirstlane(thb);
+  const uint32_t key_b = pk_key(bmax);
+
+  // ---- row bounds. Every block stores its max key and top-KB threshold in
+  // its own slot; a wave first filters with its block's own bounds and reads
+  // the row's slots (those of the blocks that got there first) only if it
+  // would keep more than WCAP elements. Any subset of the slots gives valid
+  // (if weaker) bounds, so relaxed agent-scope stores and loads suffice,
+  // nothing waits, and no address is contended.
+  uint64_t* const slots = A.slots + (int64_t)row * MAX_SEGMENTS;
+  if (tid == 0)
+    __hip_atomic_store(slots + seg, ((uint64_t)th1 << 32) | (uint64_t)key_b, __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_AGENT);
+  uint32_t mkey = key_b;
+  uint32_t theta = A.force_dense ? 0xffffffffu : row_threshold(plan, P, key2f(mkey), th1);
+  // survivors of this lane as a bit mask; run = survivors of the wave
+  float thf = key_threshold_float(theta);
+  uint32_t keep = 0;
+#pragma unroll
+  for (int i = 0; i < EPT; ++i) keep |= (val[i] >= thf ? 1u : 0u) << i;
+  uint32_t run = (uint32_t)__builtin_amdgcn_readfirstlane(wave_sum_int(__popc(keep)));
+  // at most two reads of the slots, the second after a short sleep that lets
+  // more of the row's blocks publish; a wave still over WCAP is re-read by
+  // the finisher
+  for (int attempt = 0; attempt < 2 && run > (uint32_t)WCAP && !A.force_dense; ++attempt) {
+    if (attempt > 0) __builtin_amdgcn_s_sleep(127);
+    uint32_t hm = key_b, hk = th1;
+    for (int s0 = 0; s0 < S; s0 += 64) {
+      if (s0 + lane < S) {
+        const uint64_t v = __hip_atomic_load(slots + s0 + lane, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        hm = (uint32_t)v > hm ? (uint32_t)v : hm;
+        hk = (uint32_t)(v >> 32) > hk ? (uint32_t)(v >> 32) : hk;
+      }
+    }
+    hm = wave_max_u32(hm);
+    hk = wave_max_u32(hk);
+    mkey = (uint32_t)__builtin_amdgcn_readfirstlane(hm);
+    theta = row_threshold(plan, P, key2f(mkey), (uint32_t)__builtin_amdgcn_readfirstlane(hk));
+    thf = key_threshold_float(theta);
+    keep = 0;
+#pragma unroll
+    for (int i = 0; i < EPT; ++i) keep |= (val[i] >= thf ? 1u : 0u) << i;
+    run = (uint32_t)__builtin_amdgcn_readfirstlane(wave_sum_int(__popc(keep)));
+  }
+  const float m_ref = key2f(mkey);
+
+  // ---- logprob mass relative to m_ref (terms below m_ref - ZMASS left out).
+  // Terms are binary32 exponentials accumulated in binary64: next to the
+  // row maximum's term (1.0) the small terms must not be rounded away, since
+  // the top token's logprob is -log(1 + their sum).
+  double wmass = 0.0;
+  if (A.want_mass) {
+    const float lo = m_ref - ZMASS;
+    double acc = 0.0;
+#pragma unroll
+    for (int q = 0; q < NGRP; ++q) {
+      bool any = false;
+#pragma unroll
+      for (int c = 0; c < GRP; ++c) any |= val[q * GRP + c] >= lo;
+      if (__ballot(any)) {
+#pragma unroll
+        for (int c = 0; c < GRP; ++c) {
+          const float v = val[q * GRP + c];
+          const float t = v >= lo ? (v - m_ref) * 1.4426950408889634f : -__builtin_inff();
+          acc += (double)__builtin_amdgcn_exp2f(t);
+        }
+      }
+    }
+    wmass = wave_sum_f64(acc);
+  }
+
+  // ---- hand over the survivors (or nothing if more than WCAP) -----------
+  if (run <= (uint32_t)WCAP && run > 0) {
+    const uint32_t mine = (uint32_t)__popc(keep);
+    uint32_t slot = (uint32_t)wave_incl_scan((int)mine, lane) - mine;
+    // uniform base, 32-bit per-lane slot: one register for the address
+    uint64_t* const base = A.wave_cand + (((int64_t)row * S + seg) * NWS + wave) * WCAP;
+#pragma unroll
+    for (int q = 0; q < NGRP; ++q) {
+#pragma unroll
+      for (int c = 0; c < GRP; ++c) {
+        if ((keep >> (q * GRP + c)) & 1u)
+          base[slot++] = pack(f2key(__float_as_uint(val[q * GRP + c])), ebase + q * 64 * GRP + c);
+      }
+    }
+  }
+  if (lane == 0) {
+    WaveRec r;
+    r.maxp = wmax;
+    r.mass = wmass;
+    r.mref = m_ref;
+    r.count = run <= (uint32_t)WCAP ? run : RESCAN;
+    r.th1 = th1;
+    r.flags = wflags;
+    A.wave_rec[((int64_t)row * S + seg) * NWS + wave] = r;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Descending bitonic sort of n <= CAP packed candidates held in LDS `a`.
+// Element i = r * NT + tid lives in register v[r] of its thread. A
+// compare-exchange stage with partner distance j runs through wave shuffles
+// for j < 64, inside a thread's registers for j >= NT, and through LDS (two
+// barriers) only for 64 <= j < NT.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ uint64_t cx_pick(uint64_t mine, uint64_t other, uint32_t i, uint32_t j,
+                                            uint32_t k) {
+  // descending network: the lower index of a pair in a "descending" block
+  // (i & k == 0) keeps the larger value
+  const bool take_max = ((i & j) == 0) == ((i & k) == 0);
+  return take_max ? (mine > other ? mine : other) : (mine < other ? mine : other);
+}
+
+__device__ void sort_desc(uint64_t* a, int n) {
+  const int tid = threadIdx.x;
+  int n2 = NT;
+  while (n2 < n) n2 <<= 1;
+  const int R = n2 / NT;  // 1..8
+  uint64_t v[CAP / NT];
+#pragma unroll
+  for (int r = 0; r < CAP / NT; ++r) {
+    const int i = r * NT + tid;
+    v[r] = (r < R && i < n) ? a[i] : 0ull;
+  }
+  for (int k = 2; k <= n2; k <<= 1) {
+    for (int j = k >> 1; j > 0; j >>= 1) {
+      if (j >= NT) {
+        const int jr = j / NT;
+#pragma unroll
+        for (int r = 0; r < CAP / NT; ++r) {
+          // pairs (r, r ^ jr) inside the thread; handle each pair once
+#pragma unroll
+          for (int q = 1; q < CAP / NT; q <<= 1) {
+            if (q == jr && r < R && (r & q) == 0) {
+              const uint32_t i = (uint32_t)(r * NT + tid);
+              const uint64_t lo = v[r], hi = v[r | q];
+              v[r] = cx_pick(lo, hi, i, (uint32_t)j, (uint32_t)k);
+              v[r | q] = cx_pick(hi, lo, i + (uint32_t)j, (uint32_t)j, (uint32_t)k);
+            }
+          }
+        }
+      } else if (j >= 64) {
+        __syncthreads();
+#pragma unroll
+        for (int r = 0; r < CAP / NT; ++r)
+          if (r < R) a[r * NT + tid] = v[r];
+        __syncthreads();
+#pragma unroll
+        for (int r = 0; r < CAP / NT; ++r) {
+          if (r < R) {
+            const uint32_t i = (uint32_t)(r * NT + tid);
+            v[r] = cx_pick(v[r], a[i ^ (uint32_t)j], i, (uint32_t)j, (uint32_t)k);
+          }
+        }
+      } else {
+#pragma unroll
+        for (int r = 0; r < CAP / NT; ++r) {
+          if (r < R) {
+            const uint32_t i = (uint32_t)(r * NT + tid);
+            v[r] = cx_pick(v[r], __shfl_xor(v[r], j), i, (uint32_t)j, (uint32_t)k);
+          }
         }
       }
     }
   }
-  if (tid == 0) {
-    SegInfo si;
-    si.maxp = bmax;
-    si.mass = mass;
-    si.mref = m_ref;
-    si.count = overflow ? 0u : (uint32_t)total;
-    si.flags = seg_flags | (overflow ? F_OVERFLOW : 0u);
-    si.th1 = th1;
-    A.seg_info[(int64_t)row * S + seg] = si;
-  }
-
-  // ---- last block of the row finishes ------------------------------------
-  // release: this block's candidates and SegInfo reach device-coherent memory
-  // before its arrival is counted; the finisher acquires once.
   __syncthreads();
-  if (tid == 0) {
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
-    const uint32_t old = __hip_atomic_fetch_add(&A.sync[row].done, 1u, __ATOMIC_RELAXED,
-                                                __HIP_MEMORY_SCOPE_AGENT);
-    bc[5] = (old == (uint32_t)(S - 1)) ? 1u : 0u;
-    if (bc[5]) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+#pragma unroll
+  for (int r = 0; r < CAP / NT; ++r)
+    if (r < R) a[r * NT + tid] = v[r];
+  __syncthreads();
+}
+
+// Descending sort of n <= 512 packed candidates in LDS `a` (distinct
+// values), `b` is LDS scratch of n entries. n <= 64: one wave sorts in
+// registers. Otherwise each wave sorts a 64-element run in registers and
+// every element's final position is its position in its run plus, for each
+// other run, the number of larger elements there (binary search).
+__device__ __forceinline__ uint64_t wave_sort_desc_u64(uint64_t v) {
+  const uint32_t lane = threadIdx.x & 63;
+#pragma unroll
+  for (int size = 2; size <= 64; size <<= 1) {
+#pragma unroll
+    for (int j = size >> 1; j > 0; j >>= 1) v = cx_pick(v, __shfl_xor(v, j), lane, (uint32_t)j, (uint32_t)size);
+  }
+  return v;
+}
+
+__device__ void sort_desc_small(uint64_t* a, uint64_t* b, int n) {
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  if (n <= 64) {
+    if (wave == 0) {
+      const uint64_t v = wave_sort_desc_u64(lane < n ? a[lane] : 0ull);
+      if (lane < n) a[lane] = v;
+    }
+    __syncthreads();
+    return;
+  }
+  const int runs = (n + 63) / 64;
+  uint64_t v = 0ull;
+  if (wave < runs) {
+    v = wave_sort_desc_u64(tid < n ? a[tid] : 0ull);
+    a[tid] = v;  // run `wave`, descending, zeros (absent) last
   }
   __syncthreads();
-  if (!bc[5]) return;
-  if (tid == 0) {
-    RowSync* rs = A.sync + row;
-    __hip_atomic_store(&rs->arrive, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    __hip_atomic_store(&rs->done, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    __hip_atomic_store(&rs->hint_max, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    __hip_atomic_store(&rs->hint_kb, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  if (wave < runs && v != 0ull) {
+    int rank = lane;
+    for (int w = 0; w < runs; ++w) {
+      if (w == wave) continue;
+      const uint64_t* run = a + w * 64;
+      int lo = 0, hi = 64;  // first position whose value is below v
+      while (lo < hi) {
+        const int mid = (lo + hi) >> 1;
+        if (run[mid] > v) lo = mid + 1; else hi = mid;
+      }
+      rank += lo;
+    }
+    b[rank] = v;
   }
+  __syncthreads();
+  for (int i = tid; i < n; i += NT) a[i] = b[i];
+  __syncthreads();
+}
 
-  // ---- 4. finish ----------------------------------------------------------
-  // One parallel pass over the segment records (their counts go to LDS,
-  // borrowing the weight area, which is not in use yet).
-  uint32_t* s_cnt = (uint32_t*)fl.w;         // [MAX_SEGMENTS]
-  uint32_t* s_off = s_cnt + MAX_SEGMENTS;    // [MAX_SEGMENTS]
+// ---------------------------------------------------------------------------
+// smp_finish: one block per row.
+// ---------------------------------------------------------------------------
+template <int DT, bool PEN>
+__global__ __launch_bounds__(NT) void smp_finish(SmpArgs A) {
+  __shared__ FinishLds fl;
+  __shared__ uint64_t red_u64[NW];
+  __shared__ double red_f64[NW];
+  __shared__ int red_int[NW];
+  __shared__ uint32_t red_u32[NW];
+  __shared__ uint32_t bc[4];
+  __shared__ TailShared ts;
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int row = blockIdx.x;
+  const int32_t V = A.V;
+  const int W = A.S * NWS;
+  const DevParams P = A.prm[A.prm_shared ? 0 : row];
+  const RowPlan plan = make_plan(A, P);
+  uint32_t pflags = 0;
+  const RowCtx rc = make_rowctx<PEN>(A, P, row, DT == 0 ? 4 : 2, &pflags);
+  const WaveRec* recs = A.wave_rec + (int64_t)row * W;
+
+  // ---- wave records: row max, top-KB threshold, flags, counts -----------
   uint64_t rmax = 0, rkb = 0;
-  uint32_t rflags = 0;
-  for (int s = tid; s < S; s += NT) {
-    const SegInfo si = A.seg_info[(int64_t)row * S + s];
-    rmax = si.maxp > rmax ? si.maxp : rmax;
-    rkb = si.th1 > rkb ? si.th1 : rkb;
-    rflags |= si.flags;
-    s_cnt[s] = si.count;
+  uint32_t rflags = pflags;
+  for (int w = tid; w < W; w += NT) {
+    const WaveRec r = recs[w];
+    rmax = r.maxp > rmax ? r.maxp : rmax;
+    rkb = r.th1 > rkb ? r.th1 : rkb;
+    rflags |= r.flags;
+    fl.cnt[w] = r.count == RESCAN ? 0u : r.count;
+    fl.res[w] = r.count == RESCAN ? 1u : 0u;
   }
   rmax = block_max_u64(rmax, red_u64);
   rkb = block_max_u64(rkb, red_u64);
   {
-    // OR of the segment flags across the block: every decision below
-    // (status, dense or compact) must be uniform over the block's threads
+    // OR of the flags across the block: every decision below (status, dense
+    // or compact) must be uniform over the block's threads
     uint32_t f = rflags;
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) f |= __shfl_xor(f, o);
@@ -790,99 +1030,170 @@ __global__ __launch_bounds__(NT) void smp_main(SmpArgs A) {
     for (int w = 0; w < NW; ++w) f |= red_u32[w];
     rflags = f;
   }
-  int csum;
+  // exclusive scans of the counts and of the re-scan flags; thread t owns
+  // the four records 4t .. 4t+3 (W <= MAX_WAVES = 4 * NT)
+  int csum = 0, nres = 0;
   {
-    // exclusive scan of the counts; thread t owns segments 2t and 2t+1
-    const int s0 = 2 * tid, s1 = 2 * tid + 1;
-    const int c0 = s0 < S ? (int)s_cnt[s0] : 0, c1 = s1 < S ? (int)s_cnt[s1] : 0;
-    const int ex = block_excl_scan(c0 + c1, red_int, &csum);
-    if (s0 < S) s_off[s0] = (uint32_t)ex;
-    if (s1 < S) s_off[s1] = (uint32_t)(ex + c0);
+    uint32_t c4[4], r4[4];
+    int sc = 0, sr = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int w = 4 * tid + i;
+      c4[i] = w < W ? fl.cnt[w] : 0u;
+      r4[i] = w < W ? fl.res[w] : 0u;
+      sc += (int)c4[i];
+      sr += (int)r4[i];
+    }
+    const int exc = block_excl_scan(sc, red_int, &csum);
+    const int exr = block_excl_scan(sr, red_int, &nres);
+    __syncthreads();  // every read of fl.res above precedes the list writes
+    int oc = exc, orr = exr;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int w = 4 * tid + i;
+      if (w < W) {
+        fl.off[w] = (uint32_t)oc;
+        oc += (int)c4[i];
+        if (r4[i]) fl.res[orr++] = (uint32_t)w;
+      }
+    }
   }
   const float M = key2f(pk_key(rmax));
-  double logZ = 0.0, rmass = 0.0;
+  double logZ = 0.0;
   if (A.want_mass) {
     double part = 0.0;
-    for (int s = tid; s < S; s += NT) {
-      const SegInfo si = A.seg_info[(int64_t)row * S + s];
-      part += si.mass * exp((double)si.mref - (double)M);
+    for (int w = tid; w < W; w += NT) {
+      const WaveRec r = recs[w];
+      if (r.maxp) part += r.mass * exp((double)r.mref - (double)M);
     }
-    rmass = block_sum_f64(part, red_f64);
-    logZ = log(rmass);
+    logZ = log(block_sum_f64(part, red_f64));
   }
   int32_t status = ST_OK;
   if (rflags & F_INVALID) status = ST_EINVAL;
   else if (rflags & F_NONFINITE) status = ST_ENONFINITE;
 
   if (status == ST_OK) {
-    // Final threshold from exact row quantities: every block filtered with
-    // bounds no larger than these, so the survivors below are exactly the
-    // row's elements with key >= theta_f, whatever the rendezvous timing.
-    uint32_t theta_f = (uint32_t)rkb;
-    if (plan.need_rel) {
-      const uint32_t tr = relevance_key(M, P.temperature);
-      theta_f = tr < theta_f ? tr : theta_f;
+    // Final threshold from exact row quantities: every wave filtered with
+    // bounds no larger than these, so the survivors gathered below are
+    // exactly the row's elements with key >= theta_f, whatever the timing.
+    // Row-wide top-KB bound from the lane maxima the scan blocks published
+    // (distinct elements of this row, all written by this call): the KB-th
+    // largest of them has at least KB elements at or above it. At most 512
+    // are used: the `per` largest of each block.
+    uint32_t theta_pub = 0u;
+    {
+      const int S = A.S;
+      const int per = S * TOPS <= NT ? TOPS : (NT / S > 0 ? NT / S : 1);
+      const int npub = per * S < NT ? per * S : NT;
+      uint32_t* pub = (uint32_t*)fl.w;
+      if (tid == 0) bc[1] = 0u;
+      if (tid < npub) {
+        const int sg = tid / per, k = tid - sg * per;
+        pub[tid] = A.tops[((int64_t)row * MAX_SEGMENTS + sg) * TOPS + (TOPS - 1 - k)];
+      }
+      __syncthreads();
+      if (tid < npub) {
+        const uint32_t x = pub[tid];
+        if (x != 0u) {
+          int rank = 0;
+#pragma unroll 16
+          for (int i = 0; i < npub; ++i) {
+            const uint32_t y = pub[i];
+            rank += (y > x || (y == x && i < tid)) ? 1 : 0;
+          }
+          if (rank == plan.KB - 1) bc[1] = x;
+        }
+      }
+      __syncthreads();
+      theta_pub = bc[1];
     }
-    if (theta_f < 1u) theta_f = 1u;
-    bool dense = A.force_dense || (rflags & F_OVERFLOW);
+    const uint32_t theta_f =
+        row_threshold(plan, P, M, (uint32_t)rkb > theta_pub ? (uint32_t)rkb : theta_pub);
+    bool dense = A.force_dense != 0;
     const uint64_t* cand;
     double* wbuf;
     int64_t ncand = 0;
     if (!dense) {
-      // gather the survivors of every segment in one flat parallel pass
-      // (order is irrelevant: sorted next)
-      if (tid == 0) bc[6] = 0u;
+      if (tid == 0) bc[0] = 0u;
       __syncthreads();
-      const int64_t cbase = (int64_t)row * S * CAPSEG;
+      const uint64_t* wc = A.wave_cand + (int64_t)row * W * WCAP;
+      // (a) candidates handed over by the waves
       for (int i0 = 0; i0 < csum; i0 += NT) {
         const int idx = i0 + tid;
         bool keep = false;
         uint64_t p = 0;
         if (idx < csum) {
-          int lo = 0, hi = S - 1;  // largest s with s_off[s] <= idx
+          int lo = 0, hi = W - 1;  // largest w with off[w] <= idx
           while (lo < hi) {
             const int mid = (lo + hi + 1) >> 1;
-            if ((int)s_off[mid] <= idx) lo = mid; else hi = mid - 1;
+            if ((int)fl.off[mid] <= idx) lo = mid; else hi = mid - 1;
           }
-          p = A.seg_cand[cbase + (int64_t)lo * CAPSEG + (idx - (int)s_off[lo])];
+          p = wc[(int64_t)lo * WCAP + (idx - (int)fl.off[lo])];
           keep = pk_key(p) >= theta_f;
         }
         const uint64_t m = __ballot(keep);
         uint32_t base = 0;
-        if (lane == 0 && m) base = atomicAdd(&bc[6], (uint32_t)__popcll(m));
+        if (lane == 0 && m) base = atomicAdd(&bc[0], (uint32_t)__popcll(m));
         base = __shfl(base, 0);
         const uint32_t slot = base + (uint32_t)__popcll(m & ((lane == 0) ? 0ull : (~0ull >> (64 - lane))));
         if (keep && slot < (uint32_t)CAP) fl.cand[slot] = p;
       }
-      __syncthreads();
-      csum = (int)bc[6];
-      if (csum > CAP || csum < 1) dense = true;
-    }
-    if (!dense) {
-      int n2 = 1;
-      while (n2 < csum) n2 <<= 1;
-      for (int i = csum + tid; i < n2; i += NT) fl.cand[i] = 0ull;
-      __syncthreads();
-      // bitonic sort, descending
-      for (int k = 2; k <= n2; k <<= 1) {
-        for (int j = k >> 1; j > 0; j >>= 1) {
-          for (int i = tid; i < n2; i += NT) {
-            const int ixj = i ^ j;
-            if (ixj > i) {
-              const uint64_t a = fl.cand[i], b = fl.cand[ixj];
-              const bool desc = (i & k) == 0;
-              if (desc ? (a < b) : (a > b)) {
-                fl.cand[i] = b;
-                fl.cand[ixj] = a;
+      // (b) waves that handed over nothing: read their logits again, four
+      // consecutive elements per thread (one 16-byte or 8-byte load when the
+      // rows are aligned), two groups per iteration
+      const int64_t ngrp = (int64_t)nres * (WSEG / 4);
+      for (int64_t t0 = 0; t0 < ngrp; t0 += 2 * NT) {
+        uint32_t kk[2][4];
+        int64_t e0[2];
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          const int64_t t = t0 + h * NT + tid;
+          e0[h] = 0;
+#pragma unroll
+          for (int c = 0; c < 4; ++c) kk[h][c] = 0u;
+          if (t < ngrp) {
+            e0[h] = (int64_t)fl.res[t / (WSEG / 4)] * WSEG + (t % (WSEG / 4)) * 4;
+            if (!PEN && A.vec && e0[h] + 4 <= V) {
+              uint32_t b[4];
+              if (DT == 0) {
+                const uint4 q = *(const uint4*)(rc.base + e0[h] * 4);
+                b[0] = q.x; b[1] = q.y; b[2] = q.z; b[3] = q.w;
+              } else {
+                const uint2 q = *(const uint2*)(rc.base + e0[h] * 2);
+                b[0] = q.x << 16; b[1] = q.x & 0xffff0000u; b[2] = q.y << 16; b[3] = q.y & 0xffff0000u;
               }
+#pragma unroll
+              for (int c = 0; c < 4; ++c) kk[h][c] = f2key(b[c]);
+            } else {
+#pragma unroll
+              for (int c = 0; c < 4; ++c)
+                kk[h][c] = (e0[h] + c < V) ? f2key(value_bits<DT, PEN>(rc, e0[h] + c)) : 0u;
             }
           }
-          __syncthreads();
+        }
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+#pragma unroll
+          for (int c = 0; c < 4; ++c) {
+            const bool keep = kk[h][c] >= theta_f;
+            const uint64_t m = __ballot(keep);
+            uint32_t base = 0;
+            if (lane == 0 && m) base = atomicAdd(&bc[0], (uint32_t)__popcll(m));
+            base = __shfl(base, 0);
+            const uint32_t slot = base + (uint32_t)__popcll(m & ((lane == 0) ? 0ull : (~0ull >> (64 - lane))));
+            if (keep && slot < (uint32_t)CAP) fl.cand[slot] = pack(kk[h][c], (uint32_t)(e0[h] + c));
+          }
         }
       }
+      __syncthreads();
+      ncand = (int64_t)bc[0];
+      if (ncand > CAP || ncand < 1) dense = true;
+    }
+    if (!dense) {
+      if (ncand <= NT) sort_desc_small(fl.cand, (uint64_t*)fl.w, (int)ncand);
+      else sort_desc(fl.cand, (int)ncand);
       cand = fl.cand;
       wbuf = fl.w;
-      ncand = csum;
     } else {
       const uint32_t trel = relevance_key(M, P.temperature);
       ncand = dense_build<DT, PEN>(A, rc, row, trel, plan.need_rel, plan.KB, (uint32_t*)fl.cand,
@@ -892,7 +1203,7 @@ __global__ __launch_bounds__(NT) void smp_main(SmpArgs A) {
       wbuf = A.dense_w + (int64_t)row * A.dense_ld;
     }
 
-    // outputs in raw order
+    // ---- outputs in raw order ------------------------------------------
     if (A.argmax && tid == 0) A.argmax[row] = pk_id(rmax);
     if (A.top8_ids) {
       for (int i = tid; i < 8; i += NT) {
@@ -942,7 +1253,7 @@ __global__ __launch_bounds__(NT) void smp_main(SmpArgs A) {
         A.nll_out[row] = __builtin_nan("");
       }
     }
-    // token selection
+    // ---- token selection ---------------------------------------------------
     if (A.out_ids) {
       if (P.greedy) {
         const int nd = A.mode == MODE_VERIFY ? 1 : A.n_draws;
@@ -964,8 +1275,8 @@ __global__ __launch_bounds__(NT) void smp_main(SmpArgs A) {
     if (tid == 0 && A.stats) {
       atomicAdd(&A.stats[STAT_ROWS], 1ull);
       if (dense) atomicAdd(&A.stats[STAT_DENSE_ROWS], 1ull);
-      atomicAdd(&A.stats[STAT_CANDIDATES], (unsigned long long)csum);
-      if (rflags & F_TIMEOUT) atomicAdd(&A.stats[STAT_WAIT_TIMEOUTS], 1ull);
+      atomicAdd(&A.stats[STAT_RESCAN_WAVES], (unsigned long long)nres);
+      atomicAdd(&A.stats[STAT_CANDIDATES], (unsigned long long)ncand);
     }
   } else if (A.out_ids) {
     const int nd = A.mode == MODE_VERIFY ? 1 : A.n_draws;
@@ -975,6 +1286,8 @@ __global__ __launch_bounds__(NT) void smp_main(SmpArgs A) {
     A.status[row] = status;
     if (A.row_status) A.row_status[row] = status;
   }
+  // clear the row's bound slots for the next call (ordered by the kernel boundary)
+  for (int sg = tid; sg < A.S; sg += NT) A.slots[(int64_t)row * MAX_SEGMENTS + sg] = 0ull;
 
   // ---- verify: the last finished row applies the acceptance rule --------
   if (A.mode == MODE_VERIFY) {
@@ -991,7 +1304,7 @@ __global__ __launch_bounds__(NT) void smp_main(SmpArgs A) {
         for (int j = 0; j < A.rows; ++j) ok = ok && (A.status[j] == ST_OK);
         if (ok) {
           for (int j = 0; j < A.rows; ++j) {
-            const uint32_t sel = __hip_atomic_load(A.out_ids + j, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            const uint32_t sel = A.out_ids[j];
             ++emitted;
             token = sel;
             const bool matched = (j + 1 < A.rows) && A.drafts[j] == sel;
@@ -1010,7 +1323,6 @@ __global__ __launch_bounds__(NT) void smp_main(SmpArgs A) {
     }
   }
 }
-
 // ---------------------------------------------------------------------------
 // Penalty preparation: per row, sorted unique history ids with counts and a
 // membership bitmap over the vocabulary.
@@ -1105,7 +1417,10 @@ __global__ __launch_bounds__(1024) void smp_penalty_prep(PenArgs A) {
 // ---------------------------------------------------------------------------
 template <int DT, bool VEC, bool PEN>
 static hipError_t launch_t(const SmpArgs& a, hipStream_t st) {
-  hipLaunchKernelGGL((smp_main<DT, VEC, PEN>), dim3((unsigned)(a.S * a.rows)), dim3(NT), 0, st, a);
+  hipLaunchKernelGGL((smp_scan<DT, VEC, PEN>), dim3((unsigned)(a.S * a.rows)), dim3(NTS), 0, st, a);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL((smp_finish<DT, PEN>), dim3((unsigned)a.rows), dim3(NT), 0, st, a);
   return hipGetLastError();
 }
 
