@@ -39,6 +39,9 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--profile-copy", action="store_true",
                     help="run a plain device copy of the workload's size (counter calibration)")
+    ap.add_argument("--dump-logits", metavar="PATH",
+                    help="write the workload's logits (rows x V binary32, row-major) to PATH and exit; "
+                         "lib/smp_bench --logits PATH replays them without Python")
     return ap.parse_args()
 
 
@@ -84,6 +87,10 @@ def main():
 
     print(f"generating {ROWS} x {V} logits (2*t3) on the GPU", file=sys.stderr, flush=True)
     x0 = synth.large_batch(ROWS, dev)
+    if a.dump_logits:
+        x0.cpu().numpy().tofile(a.dump_logits)
+        print(json.dumps({"dumped": a.dump_logits, "rows": ROWS, "vocab": V}))
+        return
     bufs = [x0, x0.clone(), x0.clone()]
     seeds = synth.large_batch_seeds(ROWS)
     positions = torch.arange(1, ROWS + 1, dtype=torch.int64, device=dev)

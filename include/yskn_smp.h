@@ -78,6 +78,23 @@ typedef struct yskn_smp_params {
   float frequency_penalty;  /* 0 = off */
 } yskn_smp_params;
 
+/* The same parameters with binary64 fields, exactly as the Rust
+ * SamplingParameters holds them (output_head_sampler.rs:21-28), for callers
+ * whose values are not thousandths. greedy != 0 is Sampler::Greedy
+ * (output_head_sampler.rs:77-82); its other fields are then ignored. */
+typedef struct yskn_smp_params_f64 {
+  double temperature; /* finite, > 0 */
+  double top_p;       /* (0, 1] */
+  double min_p;       /* [0, 1] */
+  uint32_t top_k;     /* as yskn_smp_params.top_k */
+  int32_t greedy;
+  uint64_t seed;
+  int32_t version;
+  float repetition_penalty; /* EXTENSION, as yskn_smp_params */
+  float presence_penalty;
+  float frequency_penalty;
+} yskn_smp_params_f64;
+
 /* Optional outputs and inputs of yskn_smp_sample. Every pointer is a device
  * pointer or NULL. Replaces the optional outputs of Q35SmpArgs
  * (top_val/top_idx [rows*8], topk_val/topk_idx [rows*20]; src/q35.hpp:117-120)
@@ -130,6 +147,11 @@ void yskn_smp_destroy(yskn_smp_handle h);
  * repeated at every call against the call's V. Synchronous, like
  * yskn_set_opt's cudaMemcpy (src/engine35.cpp:946-959). */
 int yskn_smp_set_params(yskn_smp_handle h, const yskn_smp_params* params, int32_t n);
+
+/* yskn_smp_set_params with binary64 values: the Rust SamplingParameters
+ * fields as they are (output_head_sampler.rs:21-28), validated by the rules
+ * of SamplingParameters::validate (output_head_sampler.rs:56-75). */
+int yskn_smp_set_params_f64(yskn_smp_handle h, const yskn_smp_params_f64* params, int32_t n);
 
 /* Sample one token per (row, draw). Replaces launch_q35_smp
  * (src/q35.hpp:113-122; src/q35_sample.cu:210-214) and yskn-ref
@@ -204,6 +226,10 @@ int yskn_smp_get_stats(yskn_smp_handle h, uint64_t* out, int32_t n);
 /* Validate parameters on the host without a device (the reference's
  * SamplingParameters::validate, output_head_sampler.rs:56-75). */
 int yskn_smp_validate_params(const yskn_smp_params* params, int32_t vocab, uint32_t flags);
+
+/* The same for binary64 parameters (SamplingParameters::validate on the
+ * Rust fields as they are, NaN and infinities included). */
+int yskn_smp_validate_params_f64(const yskn_smp_params_f64* params, int32_t vocab, uint32_t flags);
 
 /* Library version string. */
 const char* yskn_smp_version(void);

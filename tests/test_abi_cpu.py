@@ -70,3 +70,30 @@ def test_top_k_bounds_against_vocabulary():
 def test_both_versions_validate():
     for v in (GUMBEL, INVERSE_CUMULATIVE):
         SamplingParameters(version=v).validate(100)
+
+
+# SamplingParameters::validate on binary64 fields as they are
+# (output_head_sampler.rs:56-75): NaN and infinities fail every range check.
+@pytest.mark.parametrize("kw,msg", [
+    (dict(temperature=0.0), "temperature"), (dict(temperature=-1.0), "temperature"),
+    (dict(temperature=float("nan")), "temperature"), (dict(temperature=float("inf")), "temperature"),
+    (dict(top_p=0.0), "top_p"), (dict(top_p=1.0000000000000002), "top_p"),
+    (dict(top_p=float("nan")), "top_p"),
+    (dict(min_p=-5e-324), "min_p"), (dict(min_p=1.0000000000000002), "min_p"),
+    (dict(min_p=float("nan")), "min_p"),
+    (dict(top_k=0), "top_k"), (dict(top_k=21), "top_k"),
+])
+def test_binary64_parameters_follow_the_reference_rules(kw, msg):
+    from yskn_smp import SamplingParametersF64
+    with pytest.raises(InvalidInput) as e:
+        SamplingParametersF64(**kw).validate(248_320)
+    assert msg in str(e.value)
+
+
+def test_binary64_parameters_accept_the_reference_ranges():
+    from yskn_smp import SamplingParametersF64
+    SamplingParametersF64().validate(248_320)                     # the reference defaults
+    SamplingParametersF64(temperature=5e-324, top_p=5e-324, min_p=1.0, top_k=20).validate(20)
+    SamplingParametersF64(temperature=0.7123456789, top_p=1.0, min_p=0.0, top_k=1).validate(1)
+    # greedy (Sampler::Greedy) carries no sampling parameters to validate
+    SamplingParametersF64(temperature=float("nan"), greedy=True).validate(1)

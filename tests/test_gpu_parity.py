@@ -164,6 +164,41 @@ def test_extended_top_k(small_dev, k):
         assert list(to_u32(out["ids"]).reshape(-1)) == ref
 
 
+def test_binary64_parameters(small_dev):
+    """yskn_smp_set_params_f64: the Rust SamplingParameters fields as they are.
+    Values that are thousandths give the thousandths path's ids; arbitrary
+    binary64 values match the oracle run with the same binary64 values."""
+    from yskn_smp import SamplingParametersF64
+    rng = np.random.default_rng(64)
+    x = (2.5 * rng.standard_normal((8, 30_000))).astype(np.float32)
+    xt = torch.from_numpy(x).to(DEV)
+    pos = rng.integers(0, 10 ** 6, 8)
+    for version in (GUMBEL, INVERSE_CUMULATIVE):
+        sp = SamplingParameters(temperature_milli=700, top_p_milli=900, min_p_milli=50, top_k=20,
+                                seed=99, version=version)
+        small_dev.set_params(sp)
+        a = to_u32(_run(small_dev, xt, pos)["ids"])
+        small_dev.set_params(SamplingParametersF64(temperature=700 / 1000.0, top_p=900 / 1000.0,
+                                                   min_p=50 / 1000.0, top_k=20, seed=99,
+                                                   version=version))
+        b = to_u32(_run(small_dev, xt, pos)["ids"])
+        assert list(a) == list(b)
+        odd = [SamplingParametersF64(temperature=0.3 + 0.1234567 * r, top_p=0.8 + 0.0246813 * r,
+                                     min_p=0.0123457 * r, top_k=[1, 7, 20, 13][r % 4],
+                                     seed=5000 + r, version=version, greedy=(r == 5))
+               for r in range(8)]
+        small_dev.set_params(odd)
+        got = to_u32(_run(small_dev, xt, pos)["ids"])
+
+        def ref(r):
+            q = odd[r]
+            if q.greedy:
+                return O.greedy(x[r])
+            return O.sample(x[r], int(pos[r]), O.params(q.temperature, q.top_p, q.top_k, q.min_p,
+                                                        q.seed, q.version))
+        assert list(got.reshape(-1)) == pmap(ref, range(8))
+
+
 def test_per_row_parameters_and_greedy_rows(small_dev):
     rng = np.random.default_rng(9)
     rows = 12

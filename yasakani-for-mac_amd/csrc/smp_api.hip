@@ -40,7 +40,7 @@ struct yskn_smp {
   uint32_t flags = 0;
   int32_t max_segments = 0;
   int device = 0;
-  std::vector<yskn_smp_params> params;  // host copy, 1 or max_rows entries
+  std::vector<DevParams> params;  // host copy of the device parameters, 1 or max_rows entries
   bool params_shared = true;
   DevParams* d_params = nullptr;
   uint64_t* d_wave_cand = nullptr;
@@ -90,27 +90,6 @@ bool finite_f(float x) {
   return (b & 0x7f800000u) != 0x7f800000u;
 }
 
-int validate(const yskn_smp_params& p, int64_t vocab, uint32_t flags) {
-  if (p.temperature_milli != 0) {
-    // T = temperature_milli / 1000.0 is finite and positive by construction.
-    if (p.top_p_milli < 1 || p.top_p_milli > 1000)
-      return fail(YSKN_SMP_EINVAL, "invalid input: top_p must be in (0, 1]");
-    if (p.min_p_milli > 1000) return fail(YSKN_SMP_EINVAL, "invalid input: min_p must be in [0, 1]");
-    if (flags & YSKN_SMP_FLAG_EXTENDED_TOP_K) {
-      if ((int64_t)p.top_k > vocab)
-        return fail(YSKN_SMP_EINVAL, "invalid input: top_k must be in 0..=vocabulary size");
-    } else if (p.top_k == 0 || p.top_k > 20 || (int64_t)p.top_k > vocab) {
-      return fail(YSKN_SMP_EINVAL, "invalid input: top_k must be in 1..=min(20, vocabulary size)");
-    }
-    if (p.version != YSKN_SMP_VERSION_GUMBEL && p.version != YSKN_SMP_VERSION_INVERSE_CDF)
-      return fail(YSKN_SMP_EINVAL, "invalid input: version must be 2 or 3");
-  }
-  if (!finite_f(p.repetition_penalty) || !(p.repetition_penalty > 0.0f) ||
-      !finite_f(p.presence_penalty) || !finite_f(p.frequency_penalty))
-    return fail(YSKN_SMP_EINVAL, "invalid input: penalties must be finite, repetition > 0");
-  return YSKN_SMP_OK;
-}
-
 DevParams to_device(const yskn_smp_params& p) {
   DevParams d;
   std::memset(&d, 0, sizeof d);
@@ -130,6 +109,67 @@ DevParams to_device(const yskn_smp_params& p) {
                    ? 1
                    : 0;
   return d;
+}
+
+DevParams to_device(const yskn_smp_params_f64& p) {
+  DevParams d;
+  std::memset(&d, 0, sizeof d);
+  d.temperature = p.temperature;
+  d.top_p = p.top_p;
+  d.min_p = p.min_p;
+  d.seed = p.seed;
+  d.top_k = p.top_k;
+  d.version = p.version;
+  d.greedy = p.greedy ? 1 : 0;
+  d.rep = p.repetition_penalty;
+  d.pres = p.presence_penalty;
+  d.freq = p.frequency_penalty;
+  d.penalize = (p.repetition_penalty != 1.0f || p.presence_penalty != 0.0f ||
+                p.frequency_penalty != 0.0f)
+                   ? 1
+                   : 0;
+  return d;
+}
+
+bool finite_d(double x) { return x - x == 0.0; }
+
+// SamplingParameters::validate (output_head_sampler.rs:56-75), same order and
+// messages; greedy rows are not validated (Sampler::Greedy has no parameters),
+// penalties are the extension's.
+int validate(const DevParams& p, int64_t vocab, uint32_t flags) {
+  if (!p.greedy) {
+    if (!finite_d(p.temperature) || !(p.temperature > 0.0))
+      return fail(YSKN_SMP_EINVAL, "invalid input: temperature must be finite and positive");
+    if (!finite_d(p.top_p) || !(p.top_p > 0.0) || p.top_p > 1.0)
+      return fail(YSKN_SMP_EINVAL, "invalid input: top_p must be in (0, 1]");
+    if (!finite_d(p.min_p) || !(p.min_p >= 0.0 && p.min_p <= 1.0))
+      return fail(YSKN_SMP_EINVAL, "invalid input: min_p must be in [0, 1]");
+    if (flags & YSKN_SMP_FLAG_EXTENDED_TOP_K) {
+      if ((int64_t)p.top_k > vocab)
+        return fail(YSKN_SMP_EINVAL, "invalid input: top_k must be in 0..=vocabulary size");
+    } else if (p.top_k == 0 || p.top_k > 20 || (int64_t)p.top_k > vocab) {
+      return fail(YSKN_SMP_EINVAL, "invalid input: top_k must be in 1..=min(20, vocabulary size)");
+    }
+    if (p.version != YSKN_SMP_VERSION_GUMBEL && p.version != YSKN_SMP_VERSION_INVERSE_CDF)
+      return fail(YSKN_SMP_EINVAL, "invalid input: version must be 2 or 3");
+  }
+  if (!finite_f(p.rep) || !(p.rep > 0.0f) || !finite_f(p.pres) || !finite_f(p.freq))
+    return fail(YSKN_SMP_EINVAL, "invalid input: penalties must be finite, repetition > 0");
+  return YSKN_SMP_OK;
+}
+
+int validate(const yskn_smp_params& p, int64_t vocab, uint32_t flags) {
+  if (p.temperature_milli != 0) {
+    // thousandths are range-checked before the division
+    if (p.top_p_milli < 1 || p.top_p_milli > 1000)
+      return fail(YSKN_SMP_EINVAL, "invalid input: top_p must be in (0, 1]");
+    if (p.min_p_milli > 1000) return fail(YSKN_SMP_EINVAL, "invalid input: min_p must be in [0, 1]");
+  }
+  return validate(to_device(p), vocab, flags);
+}
+
+int validate(const yskn_smp_params_f64& p, int64_t vocab, uint32_t flags) {
+  return validate(to_device(p), vocab, flags);
 }
 
 template <typename T>
@@ -164,9 +204,7 @@ int check_params_for(yskn_smp_handle h, int32_t rows, int32_t vocab) {
 bool any_penalty(yskn_smp_handle h, int32_t rows) {
   const int n = h->params_shared ? 1 : rows;
   for (int r = 0; r < n; ++r) {
-    const yskn_smp_params& p = h->params[r];
-    if (p.repetition_penalty != 1.0f || p.presence_penalty != 0.0f || p.frequency_penalty != 0.0f)
-      return true;
+    if (h->params[r].penalize) return true;
   }
   return false;
 }
@@ -248,6 +286,11 @@ int yskn_smp_validate_params(const yskn_smp_params* params, int32_t vocab, uint3
   return validate(*params, vocab, flags);
 }
 
+int yskn_smp_validate_params_f64(const yskn_smp_params_f64* params, int32_t vocab, uint32_t flags) {
+  if (!params) return fail(YSKN_SMP_EINVAL, "invalid input: null params");
+  return validate(*params, vocab, flags);
+}
+
 int yskn_smp_create(int32_t max_rows, int32_t max_vocab, uint32_t flags, yskn_smp_handle* out) {
   if (!out) return fail(YSKN_SMP_EINVAL, "invalid input: null output handle");
   *out = nullptr;
@@ -261,7 +304,7 @@ int yskn_smp_create(int32_t max_rows, int32_t max_vocab, uint32_t flags, yskn_sm
   h->max_vocab = max_vocab;
   h->flags = flags;
   h->max_segments = (max_vocab + SEG - 1) / SEG;
-  h->params.assign(1, default_params());
+  h->params.assign(1, to_device(default_params()));
   h->params_shared = true;
   if (hipGetDevice(&h->device) != hipSuccess) h->device = 0;
   const size_t R = (size_t)max_rows, Sg = (size_t)h->max_segments;
@@ -296,8 +339,7 @@ int yskn_smp_create(int32_t max_rows, int32_t max_vocab, uint32_t flags, yskn_sm
   if (e == hipSuccess) step(hipMemset(h->d_pen_len, 0, R * sizeof(int32_t)));
   if (e == hipSuccess) step(hipMemset(h->d_stats, 0, STAT_COUNT * sizeof(unsigned long long)));
   if (e == hipSuccess) {
-    const DevParams d = to_device(h->params[0]);
-    step(hipMemcpy(h->d_params, &d, sizeof d, hipMemcpyHostToDevice));
+    step(hipMemcpy(h->d_params, h->params.data(), sizeof(DevParams), hipMemcpyHostToDevice));
   }
   if (e != hipSuccess) {
     yskn_smp_destroy(h);
@@ -319,7 +361,12 @@ void yskn_smp_destroy(yskn_smp_handle h) {
   delete h;
 }
 
-int yskn_smp_set_params(yskn_smp_handle h, const yskn_smp_params* params, int32_t n) {
+extern "C++" {
+namespace {
+
+// Validated device parameters -> handle (host copy + device copy).
+template <typename P>
+int set_params_impl(yskn_smp_handle h, const P* params, int32_t n, const char* what) {
   if (!h || !params) return fail(YSKN_SMP_EINVAL, "invalid input: null handle or params");
   if (n != 1 && (n < 1 || n > h->max_rows))
     return fail(YSKN_SMP_EINVAL, "invalid input: n must be 1 or 1..=max_rows");
@@ -332,10 +379,21 @@ int yskn_smp_set_params(yskn_smp_handle h, const yskn_smp_params* params, int32_
   // Like the reference setter: drain outstanding work, then copy.
   hipError_t e = hipDeviceSynchronize();
   if (e == hipSuccess) e = hipMemcpy(h->d_params, d.data(), n * sizeof(DevParams), hipMemcpyHostToDevice);
-  if (e != hipSuccess) return hip_fail(e, "yskn_smp_set_params");
-  h->params.assign(params, params + n);
+  if (e != hipSuccess) return hip_fail(e, what);
+  h->params.assign(d.begin(), d.end());
   h->params_shared = n == 1;
   return YSKN_SMP_OK;
+}
+
+}  // namespace
+}  // extern "C++"
+
+int yskn_smp_set_params(yskn_smp_handle h, const yskn_smp_params* params, int32_t n) {
+  return set_params_impl(h, params, n, "yskn_smp_set_params");
+}
+
+int yskn_smp_set_params_f64(yskn_smp_handle h, const yskn_smp_params_f64* params, int32_t n) {
+  return set_params_impl(h, params, n, "yskn_smp_set_params_f64");
 }
 
 int yskn_smp_sample(yskn_smp_handle h, const void* logits, int32_t dtype, int32_t rows,

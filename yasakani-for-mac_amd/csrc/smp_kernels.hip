@@ -2,28 +2,31 @@
 //
 // Two launches per call (three with penalties):
 //
-//  smp_scan   S * rows blocks of 8 wave64s. Each wave owns 2,048 consecutive
-//             logits of a row in registers (32 per lane, coalesced 16-byte
-//             loads) and works on them without waiting for anyone:
-//             order-preserving 32-bit keys, wave max, a top-KB threshold,
-//             one block barrier to share both, then per wave an agent-scope
-//             atomic max that returns the row's running bounds. With them
-//             the wave keeps only elements that can matter to the reference
-//             algorithm -- (a) elements whose binary64 weight
-//             exp_d((l - M)/T) can reach 2^-53 (smaller weights are absorbed
-//             by the reference's serial binary64 sums, whose running value is
-//             >= 1) and (b) a superset of the row's top-KB by value -- and
-//             hands them to its row's finisher. A wave that would hand over
-//             more than WCAP elements hands over none and is re-read by the
-//             finisher instead.
-//  smp_finish one block per row. Exact row maximum and top-KB threshold from
-//             the wave records give the final threshold; the survivors (which
-//             do not depend on timing) are sorted in LDS by (value desc,
-//             id asc) and the reference's serial binary64 truncation and
-//             draw run on them (output_head_sampler.rs:136-212). Rows with
-//             more survivors than LDS holds take the exact "dense" path:
-//             radix select, stable LSD radix sort in global scratch, same
-//             tail.
+//  smp_scan   S * rows blocks of 8 wave64s (S = ceil(V / 16,384)). Each wave
+//             owns 2,048 consecutive logits of a row in registers (32 per
+//             lane, coalesced 16-byte loads). Per wave: lane maxima, the wave
+//             maximum, a top-KB threshold from the sorted lane maxima; one
+//             block barrier shares them. The block stores its bounds in its
+//             own slot (relaxed agent-scope store, no contention) and its 8
+//             largest lane maxima. Each wave then keeps only the elements
+//             that can matter to the reference algorithm: (a) elements whose
+//             binary64 weight exp_d((l - M)/T) can reach 2^-53 (smaller
+//             weights are absorbed by the reference's serial binary64 sums,
+//             whose running value is >= 1) and (b) a superset of the row's
+//             top-KB by value. If its block's bounds leave more than WCAP
+//             elements, the wave reads the slots of the row's other blocks
+//             (any subset gives valid bounds). A wave still over WCAP hands
+//             over nothing and is re-read by the finisher. The wave also sums
+//             exp(l - m) over the elements near its reference m for the
+//             logprob normaliser.
+//  smp_finish one block per row. Exact row maximum and top-KB bound from the
+//             wave records and the published lane maxima give the final
+//             threshold; the survivors (which do not depend on timing) are
+//             gathered, sorted by (value desc, id asc) and the reference's
+//             serial binary64 truncation and draw run on them
+//             (output_head_sampler.rs:136-212). Rows with more survivors than
+//             LDS holds take the exact "dense" path: radix select, stable LSD
+//             radix sort in global scratch, same tail.
 //
 // Ordering is (value desc, id asc) everywhere, as output_head_sampler.rs:
 // 124-132; -0 and +0 compare equal (keys canonicalise -0 to +0) and ties go

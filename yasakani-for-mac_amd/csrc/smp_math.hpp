@@ -159,7 +159,7 @@ __device__ __noinline__ double log_d(double value) {
 }
 
 // SplitMix64 finaliser; output_head_sampler.rs:214-219.
-__device__ __forceinline__ uint64_t mix64(uint64_t z) {
+__host__ __device__ __forceinline__ uint64_t mix64(uint64_t z) {
   z += 0x9e3779b97f4a7c15ull;
   z = (z ^ (z >> 30)) * 0xbf58476d1ce4e5b9ull;
   z = (z ^ (z >> 27)) * 0x94d049bb133111ebull;

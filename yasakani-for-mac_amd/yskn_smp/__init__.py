@@ -70,6 +70,21 @@ class CParams(C.Structure):
     ]
 
 
+class CParamsF64(C.Structure):
+    _fields_ = [
+        ("temperature", C.c_double),
+        ("top_p", C.c_double),
+        ("min_p", C.c_double),
+        ("top_k", C.c_uint32),
+        ("greedy", C.c_int32),
+        ("seed", C.c_uint64),
+        ("version", C.c_int32),
+        ("repetition_penalty", C.c_float),
+        ("presence_penalty", C.c_float),
+        ("frequency_penalty", C.c_float),
+    ]
+
+
 class CAux(C.Structure):
     _fields_ = [
         ("argmax", C.c_void_p),
@@ -91,7 +106,8 @@ EXPORTED = [
     "yskn_smp_last_error", "yskn_smp_create", "yskn_smp_destroy", "yskn_smp_set_params",
     "yskn_smp_sample", "yskn_smp_argmax", "yskn_smp_top_tokens", "yskn_smp_nll",
     "yskn_smp_verify", "yskn_smp_sync", "yskn_smp_select_host", "yskn_smp_validate_params",
-    "yskn_smp_version", "yskn_smp_get_stats",
+    "yskn_smp_version", "yskn_smp_get_stats", "yskn_smp_set_params_f64",
+    "yskn_smp_validate_params_f64",
 ]
 
 _lib = None
@@ -120,6 +136,8 @@ def load_library(path: str = LIB_PATH) -> C.CDLL:
     L.yskn_smp_sync.argtypes = [vp, vp]
     L.yskn_smp_select_host.argtypes = [vp, vp, i32, u64, C.POINTER(u32)]
     L.yskn_smp_validate_params.argtypes = [C.POINTER(CParams), i32, u32]
+    L.yskn_smp_set_params_f64.argtypes = [vp, C.POINTER(CParamsF64), i32]
+    L.yskn_smp_validate_params_f64.argtypes = [C.POINTER(CParamsF64), i32, u32]
     L.yskn_smp_get_stats.argtypes = [vp, C.POINTER(C.c_uint64), i32]
     L.yskn_smp_get_stats.restype = C.c_int
     for name in ("yskn_smp_create", "yskn_smp_set_params", "yskn_smp_sample", "yskn_smp_argmax",
@@ -186,6 +204,34 @@ class SamplingParameters:
         _raise(L.yskn_smp_validate_params(C.byref(c), vocabulary_size, flags))
 
 
+@dataclass
+class SamplingParametersF64:
+    """The Rust ``SamplingParameters`` fields as they are
+    (output_head_sampler.rs:21-28): binary64 temperature, top_p and min_p.
+    ``greedy=True`` stands for ``Sampler::Greedy``."""
+
+    temperature: float = 1.0
+    top_p: float = 0.95
+    top_k: int = 20
+    min_p: float = 0.0
+    seed: int = 0
+    version: int = GUMBEL
+    greedy: bool = False
+    repetition_penalty: float = 1.0
+    presence_penalty: float = 0.0
+    frequency_penalty: float = 0.0
+
+    def to_c(self) -> CParamsF64:
+        return CParamsF64(self.temperature, self.top_p, self.min_p, self.top_k, int(self.greedy),
+                          self.seed & 0xFFFFFFFFFFFFFFFF, self.version, self.repetition_penalty,
+                          self.presence_penalty, self.frequency_penalty)
+
+    def validate(self, vocabulary_size: int, flags: int = 0) -> None:
+        L = load_library()
+        c = self.to_c()
+        _raise(L.yskn_smp_validate_params_f64(C.byref(c), vocabulary_size, flags))
+
+
 def _ptr(t) -> Optional[int]:
     return None if t is None else t.data_ptr()
 
@@ -224,8 +270,15 @@ class DeviceSampler:
         return C.c_void_p(self.torch.cuda.current_stream().cuda_stream)
 
     def set_params(self, params) -> None:
-        if isinstance(params, SamplingParameters):
+        """One set for every row, or one per row. Thousandths sets go
+        through yskn_smp_set_params, binary64 sets through
+        yskn_smp_set_params_f64 (a list must not mix the two)."""
+        if isinstance(params, (SamplingParameters, SamplingParametersF64)):
             params = [params]
+        if all(isinstance(p, SamplingParametersF64) for p in params):
+            arr = (CParamsF64 * len(params))(*[p.to_c() for p in params])
+            _raise(self.L.yskn_smp_set_params_f64(self.h, arr, len(params)))
+            return
         arr = (CParams * len(params))(*[p.to_c() for p in params])
         _raise(self.L.yskn_smp_set_params(self.h, arr, len(params)))
 
