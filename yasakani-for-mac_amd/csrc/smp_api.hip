@@ -38,15 +38,10 @@ struct yskn_smp {
   int32_t max_rows = 0;
   int32_t max_vocab = 0;
   uint32_t flags = 0;
-  int32_t max_segments = 0;
   int device = 0;
   std::vector<DevParams> params;  // host copy of the device parameters, 1 or max_rows entries
   bool params_shared = true;
   DevParams* d_params = nullptr;
-  uint64_t* d_wave_cand = nullptr;
-  WaveRec* d_wave_rec = nullptr;
-  uint64_t* d_slots = nullptr;
-  uint32_t* d_tops = nullptr;
   int32_t* d_status = nullptr;
   uint32_t* d_vcount = nullptr;
   uint32_t* d_vresult = nullptr;
@@ -217,7 +212,6 @@ SmpArgs base_args(yskn_smp_handle h, const void* logits, int32_t rows, int32_t v
   a.ld = ld;
   a.V = vocab;
   a.rows = rows;
-  a.S = (vocab + SEG - 1) / SEG;
   a.mode = MODE_SAMPLE;
   a.prm = h->d_params;
   a.prm_shared = h->params_shared ? 1 : 0;
@@ -228,10 +222,6 @@ SmpArgs base_args(yskn_smp_handle h, const void* logits, int32_t rows, int32_t v
   a.pen_ids = h->d_pen_ids;
   a.pen_cnt = h->d_pen_cnt;
   a.pen_len = h->d_pen_len;
-  a.wave_cand = h->d_wave_cand;
-  a.wave_rec = h->d_wave_rec;
-  a.slots = h->d_slots;
-  a.tops = h->d_tops;
   a.dense_a = h->d_dense_a;
   a.dense_b = h->d_dense_b;
   a.dense_w = h->d_dense_w;
@@ -297,17 +287,16 @@ int yskn_smp_create(int32_t max_rows, int32_t max_vocab, uint32_t flags, yskn_sm
   if (max_rows <= 0) return fail(YSKN_SMP_EINVAL, "invalid input: max_rows must be positive");
   if (max_vocab <= 0)
     return fail(YSKN_SMP_EINVAL, "invalid input: logits must contain a nonempty u32-indexed vocabulary");
-  if ((int64_t)max_vocab > (int64_t)SEG * MAX_SEGMENTS)
+  if ((int64_t)max_vocab > VMAX)
     return fail(YSKN_SMP_ERANGE, "vocabulary larger than 4,194,304");
   yskn_smp* h = new yskn_smp();
   h->max_rows = max_rows;
   h->max_vocab = max_vocab;
   h->flags = flags;
-  h->max_segments = (max_vocab + SEG - 1) / SEG;
   h->params.assign(1, to_device(default_params()));
   h->params_shared = true;
   if (hipGetDevice(&h->device) != hipSuccess) h->device = 0;
-  const size_t R = (size_t)max_rows, Sg = (size_t)h->max_segments;
+  const size_t R = (size_t)max_rows;
   h->dense_ld = ((int64_t)max_vocab + 63) / 64 * 64;
   h->bm_ld = ((int64_t)max_vocab + 31) / 32;
   hipError_t e = hipSuccess;
@@ -315,10 +304,6 @@ int yskn_smp_create(int32_t max_rows, int32_t max_vocab, uint32_t flags, yskn_sm
     if (e == hipSuccess) e = r;
   };
   step(alloc(&h->d_params, R));
-  step(alloc(&h->d_wave_cand, R * Sg * NWS * WCAP));
-  step(alloc(&h->d_wave_rec, R * Sg * NWS));
-  step(alloc(&h->d_slots, R * (size_t)MAX_SEGMENTS));
-  step(alloc(&h->d_tops, R * (size_t)MAX_SEGMENTS * TOPS));
   step(alloc(&h->d_status, R));
   step(alloc(&h->d_vcount, 4));
   step(alloc(&h->d_vresult, 4));
@@ -333,7 +318,6 @@ int yskn_smp_create(int32_t max_rows, int32_t max_vocab, uint32_t flags, yskn_sm
   step(alloc(&h->d_host_logits, (size_t)max_vocab));
   step(alloc(&h->d_host_pos, 1));
   step(alloc(&h->d_host_out, 1));
-  if (e == hipSuccess) step(hipMemset(h->d_slots, 0, R * (size_t)MAX_SEGMENTS * sizeof(uint64_t)));
   if (e == hipSuccess) step(hipMemset(h->d_status, 0, R * sizeof(int32_t)));
   if (e == hipSuccess) step(hipMemset(h->d_vcount, 0, 4 * sizeof(uint32_t)));
   if (e == hipSuccess) step(hipMemset(h->d_pen_len, 0, R * sizeof(int32_t)));
@@ -351,7 +335,7 @@ int yskn_smp_create(int32_t max_rows, int32_t max_vocab, uint32_t flags, yskn_sm
 
 void yskn_smp_destroy(yskn_smp_handle h) {
   if (!h) return;
-  void* ptrs[] = {h->d_params,     h->d_wave_cand, h->d_wave_rec,    h->d_slots,    h->d_tops,
+  void* ptrs[] = {h->d_params,
                   h->d_status,     h->d_vcount,    h->d_vresult,     h->d_dense_a,
                   h->d_dense_b,    h->d_dense_w,   h->d_pen_bitmap,  h->d_pen_ids,
                   h->d_pen_cnt,    h->d_pen_len,   h->d_stats,       h->d_host_logits,

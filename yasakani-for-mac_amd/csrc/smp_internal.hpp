@@ -6,26 +6,20 @@
 
 namespace yskn {
 
-// Scan geometry. A scan block of 8 wave64s owns a 16,384-element segment of
-// a row; each wave owns 2,048 consecutive elements (32 per lane, coalesced
-// 16-byte loads), held in registers. A row of V logits spans S = ceil(V/SEG)
-// scan blocks and W = 8 * S wave records. The finisher uses 8 waves per row.
-constexpr int NTS = 512;           // threads per scan block (8 wave64s)
-constexpr int NWS = NTS / 64;      // waves per scan block
-constexpr int NT = 512;            // threads per finisher block (8 wave64s)
-constexpr int NW = NT / 64;        // waves per finisher block
-constexpr int EPT = 32;            // elements per lane
-constexpr int WSEG = 64 * EPT;     // elements per wave
-constexpr int SEG = NTS * EPT;     // elements per scan block
-constexpr int WCAP = 256;          // candidates a wave may hand to its row's finisher
-constexpr int CAP = 4096;          // candidates the finisher sorts in LDS
+// Geometry. One block of 8 wave64s per row; each wave streams the row's
+// 2,048-logit chunks w, w + 8, w + 16, ... (32 values per lane, coalesced
+// 16-byte loads, two chunks in flight).
+constexpr int NT = 512;            // threads per row block (8 wave64s)
+constexpr int NW = NT / 64;        // waves per row block
+constexpr int EPT = 32;            // elements per lane per chunk
+constexpr int WSEG = 64 * EPT;     // elements per chunk
+constexpr int CAP = 4096;          // candidates a row block sorts in LDS
+constexpr int BUFCAP = 8192;       // candidates a row block's append buffer holds
+constexpr int DCHUNK = 64;         // survivors above which a chunk is deferred
+constexpr int DEFCAP = 1024;       // deferred chunks a row block records
 constexpr int KBMAX = 64;          // largest "small" top-k / list length
 constexpr int HCAP = 16384;        // history tokens per row for the penalties
-constexpr int MAX_SEGMENTS = 256;  // V <= 4,194,304
-constexpr int MAX_WAVES = MAX_SEGMENTS * NWS;
-constexpr uint32_t RESCAN = 0xffffffffu;  // wave record count: finisher re-scans the wave
-constexpr int TOPS = 8;            // lane maxima each scan block publishes (NWS * TOPS == 64)
-static_assert(NWS * TOPS == 64, "one wave merges the block's published lane maxima");
+constexpr int64_t VMAX = 4194304;  // largest vocabulary
 
 // Binary64 log-domain cut for the serial-sum argument: a weight exp_d(z)
 // with z < -37.5 is below 2^-53 and cannot change a running binary64 sum
@@ -58,25 +52,11 @@ struct DevParams {
   int32_t pad;
 };
 
-// What a wave hands to its row's finisher (32 bytes).
-struct WaveRec {
-  uint64_t maxp;   // packed (key << 32) | ~id of the wave's largest logit (0: no elements)
-  double mass;     // sum of exp(l - mref) over the wave's elements with l >= mref - ZMASS
-  float mref;      // reference point of mass
-  uint32_t count;  // candidates written (<= WCAP) or RESCAN
-  uint32_t th1;    // the block's top-KB threshold key
-  uint32_t flags;  // F_*
-};
-
-// Per-block bound slots: slot (row, seg) holds (top-KB threshold key << 32 |
-// block max key) once the block has published it, 0 otherwise. Zero between
-// calls (the finisher clears its row).
-
 // Counters for profiling the path (cumulative since create).
 enum StatIndex {
   STAT_ROWS = 0,      // rows finished
   STAT_DENSE_ROWS,    // rows served by the exact large-candidate path
-  STAT_RESCAN_WAVES,  // wave segments the finishers re-read
+  STAT_RESCAN_WAVES,  // always 0 (kept for the counter layout of the C ABI)
   STAT_CANDIDATES,    // survivors sorted by finishers
   STAT_COUNT
 };
@@ -88,7 +68,6 @@ struct SmpArgs {
   int64_t ld;  // elements between rows
   int32_t V;
   int32_t rows;
-  int32_t S;   // scan blocks per row
   int32_t mode;
   const DevParams* prm;
   int32_t prm_shared;
@@ -119,10 +98,6 @@ struct SmpArgs {
   const uint32_t* pen_cnt;     // [rows][HCAP]
   const int32_t* pen_len;      // [rows], -1 = invalid history
   // workspace
-  uint64_t* wave_cand;  // [rows][S * NWS][WCAP]
-  WaveRec* wave_rec;    // [rows][S * NWS]
-  uint64_t* slots;      // [rows][MAX_SEGMENTS]
-  uint32_t* tops;       // [rows][MAX_SEGMENTS][TOPS] each block's largest lane maxima
   uint64_t* dense_a;    // [rows][dense_ld]
   uint64_t* dense_b;
   double* dense_w;

@@ -1,32 +1,24 @@
 // smp_kernels.hip -- gfx950 kernels of the per-step sampling path.
 //
-// Two launches per call (three with penalties):
+// One launch per call (two with penalties):
 //
-//  smp_scan   S * rows blocks of 8 wave64s (S = ceil(V / 16,384)). Each wave
-//             owns 2,048 consecutive logits of a row in registers (32 per
-//             lane, coalesced 16-byte loads). Per wave: lane maxima, the wave
-//             maximum, a top-KB threshold from the sorted lane maxima; one
-//             block barrier shares them. The block stores its bounds in its
-//             own slot (relaxed agent-scope store, no contention) and its 8
-//             largest lane maxima. Each wave then keeps only the elements
-//             that can matter to the reference algorithm: (a) elements whose
+//  smp_row    one block of 8 wave64s per row. The waves stream the row in
+//             2,048-logit chunks (32 values per lane, coalesced 16-byte
+//             loads, two chunks in flight) and keep only the elements that
+//             can matter to the reference algorithm: (a) elements whose
 //             binary64 weight exp_d((l - M)/T) can reach 2^-53 (smaller
 //             weights are absorbed by the reference's serial binary64 sums,
 //             whose running value is >= 1) and (b) a superset of the row's
-//             top-KB by value. If its block's bounds leave more than WCAP
-//             elements, the wave reads the slots of the row's other blocks
-//             (any subset gives valid bounds). A wave still over WCAP hands
-//             over nothing and is re-read by the finisher. The wave also sums
-//             exp(l - m) over the elements near its reference m for the
-//             logprob normaliser.
-//  smp_finish one block per row. Exact row maximum and top-KB bound from the
-//             wave records and the published lane maxima give the final
-//             threshold; the survivors (which do not depend on timing) are
-//             gathered, sorted by (value desc, id asc) and the reference's
-//             serial binary64 truncation and draw run on them
-//             (output_head_sampler.rs:136-212). Rows with more survivors than
-//             LDS holds take the exact "dense" path: radix select, stable LSD
-//             radix sort in global scratch, same tail.
+//             top-KB by value. The row's running maximum and top-KB bound
+//             live in LDS, so every wave filters with the row's bounds as they
+//             stand; the kept elements go to an LDS candidate buffer, which
+//             the block then sorts by (value desc, id asc) before running the
+//             reference's serial binary64 truncation and draw
+//             (output_head_sampler.rs:136-212). Rows with more candidates
+//             than LDS holds take the exact "dense" path: radix select, stable
+//             LSD radix sort in global scratch, same tail.
+//  smp_penalty_prep (penalties only) sorts each row's history into unique
+//             ids, counts and a membership bitmap.
 //
 // Ordering is (value desc, id asc) everywhere, as output_head_sampler.rs:
 // 124-132; -0 and +0 compare equal (keys canonicalise -0 to +0) and ties go
@@ -105,6 +97,31 @@ __device__ __forceinline__ uint32_t wave_min_u32(uint32_t v) {
     v = v < w ? v : w;
   }
   return v;
+}
+// Wave-wide maximum through DPP (VALU only, no LDS round trips): an
+// inclusive max-scan inside each row of 16 lanes (row_shr 1, 2, 4, 8; lanes
+// shifted in from outside the row read 0, the identity), then row_bcast:15
+// and row_bcast:31 carry the rows' totals upward. Lane 63 ends with the
+// maximum of all 64 lanes; it is returned (uniform) to every lane.
+template <int CTRL, int ROWS>
+__device__ __forceinline__ uint32_t dpp_u32(uint32_t v) {
+  return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, ROWS, 0xf, false);
+}
+__device__ __forceinline__ uint32_t wave_max_dpp(uint32_t v) {
+  uint32_t t;
+  t = dpp_u32<0x111, 0xf>(v); v = v > t ? v : t;  // row_shr:1
+  t = dpp_u32<0x112, 0xf>(v); v = v > t ? v : t;  // row_shr:2
+  t = dpp_u32<0x114, 0xf>(v); v = v > t ? v : t;  // row_shr:4
+  t = dpp_u32<0x118, 0xf>(v); v = v > t ? v : t;  // row_shr:8
+  t = dpp_u32<0x142, 0xa>(v); v = v > t ? v : t;  // row_bcast:15 into rows 1, 3
+  t = dpp_u32<0x143, 0xc>(v); v = v > t ? v : t;  // row_bcast:31 into rows 2, 3
+  return (uint32_t)__builtin_amdgcn_readlane((int)v, 63);
+}
+// Wave-wide minimum (the maximum of the complements).
+__device__ __forceinline__ uint32_t wave_min_u32_dpp(uint32_t v) { return ~wave_max_dpp(~v); }
+// Number of lanes below this one whose bit is set in the wave mask m.
+__device__ __forceinline__ uint32_t lanes_below(uint64_t m) {
+  return __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
 }
 __device__ __forceinline__ double wave_sum_f64(double v) {
 #pragma unroll
@@ -306,17 +323,6 @@ __device__ __forceinline__ uint64_t position_of(const SmpArgs& A, int row, int d
 }
 
 // ---------------------------------------------------------------------------
-// LDS layout of the finisher (88 KB); the dense path borrows `cand`.
-// ---------------------------------------------------------------------------
-struct FinishLds {
-  uint64_t cand[CAP];          // survivors, sorted (compact path)
-  double w[CAP];               // weights of the first c candidates (compact path)
-  uint32_t cnt[MAX_WAVES];     // per wave: candidates handed over (0 if re-scanned)
-  uint32_t off[MAX_WAVES];     // exclusive prefix of cnt
-  uint32_t res[MAX_WAVES];     // indices of the waves to re-scan
-};
-
-// ---------------------------------------------------------------------------
 // Truncation and draw on the first c sorted candidates (output_head_sampler.rs
 // :136-212). cand/w are generic pointers (LDS or global scratch).
 // ---------------------------------------------------------------------------
@@ -327,7 +333,7 @@ struct TailShared {
   int pick;
 };
 
-__device__ void sample_tail(const SmpArgs& A, const DevParams& P, int row, const uint64_t* cand,
+__device__ __forceinline__ void sample_tail(const SmpArgs& A, const DevParams& P, int row, const uint64_t* cand,
                             double* w, int64_t c, TailShared* ts, double* redd, int* redi,
                             uint64_t* redu) {
   const int tid = threadIdx.x;
@@ -451,7 +457,7 @@ __device__ void sample_tail(const SmpArgs& A, const DevParams& P, int row, const
 // Dense path: exact sorted order of every element with key >= theta_D.
 // ---------------------------------------------------------------------------
 template <int DT, bool PEN>
-__device__ int64_t dense_build(const SmpArgs& A, const RowCtx& rc, int row, uint32_t theta_rel,
+__device__ __forceinline__ int64_t dense_build(const SmpArgs& A, const RowCtx& rc, int row, uint32_t theta_rel,
                                bool need_rel, int KB, uint32_t* lds, int* redi) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int V = A.V;
@@ -614,251 +620,6 @@ __device__ __forceinline__ uint32_t row_threshold(const RowPlan& plan, const Dev
 }
 
 // ---------------------------------------------------------------------------
-// smp_scan: one wave per 2,048 logits.
-// ---------------------------------------------------------------------------
-template <int DT, bool VEC, bool PEN>
-__global__ __launch_bounds__(NTS) __attribute__((amdgpu_waves_per_eu(6))) void smp_scan(SmpArgs A) {
-  __shared__ uint64_t s_wmax[NWS];
-  __shared__ uint32_t s_wtb[NWS];
-  __shared__ uint32_t s_top[NWS * TOPS];
-
-  // wave index and every per-wave quantity below are uniform: keep them in
-  // scalar registers (readfirstlane) so the 32 keys own the vector file
-  const int tid = threadIdx.x, lane = tid & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int S = A.S;
-  const int32_t V = A.V;
-  // Workgroups are dealt round-robin to the 8 XCDs (linear id mod 8). Groups
-  // of 8 rows are laid out so that all S blocks of a row share one XCD: they
-  // are dispatched together by one dispatcher and their bounds arrive early.
-  int row, seg;
-  {
-    const int b = blockIdx.x;
-    const int full = (A.rows / 8) * 8;  // rows in complete groups of 8
-    if (b < full * S) {
-      const int g = b / (8 * S), r8 = b - g * 8 * S;
-      row = g * 8 + (r8 & 7);
-      seg = r8 >> 3;
-    } else {
-      const int r = b - full * S;
-      row = full + r / S;
-      seg = r - (r / S) * S;
-    }
-  }
-  const DevParams P = A.prm[A.prm_shared ? 0 : row];
-  const RowPlan plan = make_plan(A, P);
-  uint32_t wflags = 0;
-  const RowCtx rc = make_rowctx<PEN>(A, P, row, DT == 0 ? 4 : 2, &wflags);
-
-  // ---- load 32 logits per lane as raw bits ------------------------------
-  // Element of (q, c) for this lane: e = ebase + q * 64 * GRP + c (32-bit:
-  // V <= 4,194,304). A wave whose 2,048 elements are all inside the row
-  // (every wave but the row's last) runs without per-element bounds checks.
-  constexpr int GRP = (DT == 0) ? 4 : 8;  // elements per 16-byte load
-  constexpr int NGRP = EPT / GRP;
-  const uint32_t w0 = (uint32_t)seg * SEG + (uint32_t)wave * WSEG;
-  const uint32_t ebase = w0 + (uint32_t)lane * GRP;
-  const bool full = w0 + WSEG <= (uint32_t)V;
-  uint32_t key[EPT];
-  if (VEC && full) {
-    const uint4* src = (const uint4*)(rc.base + (size_t)ebase * (DT == 0 ? 4 : 2));
-#pragma unroll
-    for (int q = 0; q < NGRP; ++q) {
-      const uint4 v = src[q * 64];
-      if (DT == 0) {
-        key[q * 4 + 0] = v.x;
-        key[q * 4 + 1] = v.y;
-        key[q * 4 + 2] = v.z;
-        key[q * 4 + 3] = v.w;
-      } else {
-        key[q * 8 + 0] = v.x << 16;
-        key[q * 8 + 1] = v.x & 0xffff0000u;
-        key[q * 8 + 2] = v.y << 16;
-        key[q * 8 + 3] = v.y & 0xffff0000u;
-        key[q * 8 + 4] = v.z << 16;
-        key[q * 8 + 5] = v.z & 0xffff0000u;
-        key[q * 8 + 6] = v.w << 16;
-        key[q * 8 + 7] = v.w & 0xffff0000u;
-      }
-    }
-  } else {
-#pragma unroll
-    for (int q = 0; q < NGRP; ++q) {
-#pragma unroll
-      for (int c = 0; c < GRP; ++c) {
-        const uint32_t e = ebase + q * 64 * GRP + c;
-        key[q * GRP + c] = e < (uint32_t)V ? raw_bits<DT>(rc, e) : 0u;
-      }
-    }
-  }
-  // ---- values, lane max (first index on ties: indices grow with q, c) ---
-  // The hot loop works on binary32 values: IEEE comparisons treat -0 and +0
-  // as equal, exactly like the canonical keys; 32-bit keys are formed only
-  // for the lane maximum and for the elements handed over. Absent elements
-  // (past the row's end) are -inf, which no threshold keeps.
-  float val[EPT];
-  bool bad = false;
-  float lmax = -__builtin_inff();
-  uint32_t imax = 0;
-#pragma unroll
-  for (int q = 0; q < NGRP; ++q) {
-    uint32_t wbits = 0;
-    const uint32_t e0 = ebase + q * 64 * GRP;
-    if (PEN && rc.bitmap && e0 < (uint32_t)V) wbits = rc.bitmap[e0 >> 5];
-#pragma unroll
-    for (int c = 0; c < GRP; ++c) {
-      const uint32_t e = e0 + c;
-      uint32_t b = key[q * GRP + c];
-      float v = -__builtin_inff();
-      if (full || e < (uint32_t)V) {
-        if (PEN && rc.bitmap && ((wbits >> (e & 31)) & 1u)) b = penalize(b, pen_count(rc, e), rc);
-        v = __uint_as_float(b);
-        bad |= __builtin_amdgcn_class(v, 0x207) != 0;  // signaling/quiet NaN, +-inf
-      }
-      val[q * GRP + c] = v;
-      // track the offset (an immediate) rather than the index: no per-element
-      // index register stays live into the hand-over below
-      if (v > lmax) {
-        lmax = v;
-        imax = q * 64 * GRP + c;
-      }
-    }
-  }
-  imax += ebase;
-  if (__ballot(bad)) wflags |= F_NONFINITE;
-  const uint32_t kmax = lmax == -__builtin_inff() ? 0u : f2key(__float_as_uint(lmax));
-  const uint64_t wmax = wave_max_u64(kmax ? pack(kmax, imax) : 0ull);
-  // Top-KB threshold of the block: per wave the ceil(KB/8)-th largest lane
-  // maximum (0 where too few lanes hold data); the minimum over the block's
-  // 8 waves has at least 8 * ceil(KB/8) >= KB elements at or above it.
-  const uint32_t lsorted = wave_sort_asc(kmax);
-  const uint32_t wb = __shfl(lsorted, 64 - (plan.KB + NWS - 1) / NWS);
-  if (lane == 0) {
-    s_wmax[wave] = wmax;
-    s_wtb[wave] = wb;
-  }
-  if (lane >= 64 - TOPS) s_top[wave * TOPS + lane - (64 - TOPS)] = lsorted;
-  __syncthreads();
-  // The block publishes its TOPS largest lane maxima: distinct elements of
-  // the row, from which the finisher takes a row-wide top-KB bound.
-  if (wave == 0) {
-    const uint32_t t = wave_sort_asc(s_top[lane]);
-    if (lane >= 64 - TOPS)
-      A.tops[((int64_t)row * MAX_SEGMENTS + seg) * TOPS + lane - (64 - TOPS)] = t;
-  }
-  // lane w < 8 reads wave w's record; three shuffle steps reduce them (few
-  // registers live next to the 32 keys)
-  uint64_t bmax = lane < NWS ? s_wmax[lane] : 0ull;
-  uint32_t thb = lane < NWS ? s_wtb[lane] : 0xffffffffu;
-#pragma unroll
-  for (int o = NWS / 2; o > 0; o >>= 1) {
-    const uint64_t ob = __shfl_xor(bmax, o);
-    const uint32_t oc = __shfl_xor(thb, o);
-    bmax = ob > bmax ? ob : bmax;
-    thb = oc < thb ? oc : thb;
-  }
-  // (readfirstlane yields int: convert through uint32_t, never sign-extend)
-  bmax = ((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(bmax >> 32)) << 32) |
-         (uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)bmax);
-  const uint32_t th1 = (uint32_t)__builtin_amdgcn_readfirstlane(thb);
-  const uint32_t key_b = pk_key(bmax);
-
-  // ---- row bounds. Every block stores its max key and top-KB threshold in
-  // its own slot; a wave first filters with its block's own bounds and reads
-  // the row's slots (those of the blocks that got there first) only if it
-  // would keep more than WCAP elements. Any subset of the slots gives valid
-  // (if weaker) bounds, so relaxed agent-scope stores and loads suffice,
-  // nothing waits, and no address is contended.
-  uint64_t* const slots = A.slots + (int64_t)row * MAX_SEGMENTS;
-  if (tid == 0)
-    __hip_atomic_store(slots + seg, ((uint64_t)th1 << 32) | (uint64_t)key_b, __ATOMIC_RELAXED,
-                       __HIP_MEMORY_SCOPE_AGENT);
-  uint32_t mkey = key_b;
-  uint32_t theta = A.force_dense ? 0xffffffffu : row_threshold(plan, P, key2f(mkey), th1);
-  // survivors of this lane as a bit mask; run = survivors of the wave
-  float thf = key_threshold_float(theta);
-  uint32_t keep = 0;
-#pragma unroll
-  for (int i = 0; i < EPT; ++i) keep |= (val[i] >= thf ? 1u : 0u) << i;
-  uint32_t run = (uint32_t)__builtin_amdgcn_readfirstlane(wave_sum_int(__popc(keep)));
-  // at most two reads of the slots, the second after a short sleep that lets
-  // more of the row's blocks publish; a wave still over WCAP is re-read by
-  // the finisher
-  for (int attempt = 0; attempt < 2 && run > (uint32_t)WCAP && !A.force_dense; ++attempt) {
-    if (attempt > 0) __builtin_amdgcn_s_sleep(127);
-    uint32_t hm = key_b, hk = th1;
-    for (int s0 = 0; s0 < S; s0 += 64) {
-      if (s0 + lane < S) {
-        const uint64_t v = __hip_atomic_load(slots + s0 + lane, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        hm = (uint32_t)v > hm ? (uint32_t)v : hm;
-        hk = (uint32_t)(v >> 32) > hk ? (uint32_t)(v >> 32) : hk;
-      }
-    }
-    hm = wave_max_u32(hm);
-    hk = wave_max_u32(hk);
-    mkey = (uint32_t)__builtin_amdgcn_readfirstlane(hm);
-    theta = row_threshold(plan, P, key2f(mkey), (uint32_t)__builtin_amdgcn_readfirstlane(hk));
-    thf = key_threshold_float(theta);
-    keep = 0;
-#pragma unroll
-    for (int i = 0; i < EPT; ++i) keep |= (val[i] >= thf ? 1u : 0u) << i;
-    run = (uint32_t)__builtin_amdgcn_readfirstlane(wave_sum_int(__popc(keep)));
-  }
-  const float m_ref = key2f(mkey);
-
-  // ---- logprob mass relative to m_ref (terms below m_ref - ZMASS left out).
-  // Terms are binary32 exponentials accumulated in binary64: next to the
-  // row maximum's term (1.0) the small terms must not be rounded away, since
-  // the top token's logprob is -log(1 + their sum).
-  double wmass = 0.0;
-  if (A.want_mass) {
-    const float lo = m_ref - ZMASS;
-    double acc = 0.0;
-#pragma unroll
-    for (int q = 0; q < NGRP; ++q) {
-      bool any = false;
-#pragma unroll
-      for (int c = 0; c < GRP; ++c) any |= val[q * GRP + c] >= lo;
-      if (__ballot(any)) {
-#pragma unroll
-        for (int c = 0; c < GRP; ++c) {
-          const float v = val[q * GRP + c];
-          const float t = v >= lo ? (v - m_ref) * 1.4426950408889634f : -__builtin_inff();
-          acc += (double)__builtin_amdgcn_exp2f(t);
-        }
-      }
-    }
-    wmass = wave_sum_f64(acc);
-  }
-
-  // ---- hand over the survivors (or nothing if more than WCAP) -----------
-  if (run <= (uint32_t)WCAP && run > 0) {
-    const uint32_t mine = (uint32_t)__popc(keep);
-    uint32_t slot = (uint32_t)wave_incl_scan((int)mine, lane) - mine;
-    // uniform base, 32-bit per-lane slot: one register for the address
-    uint64_t* const base = A.wave_cand + (((int64_t)row * S + seg) * NWS + wave) * WCAP;
-#pragma unroll
-    for (int q = 0; q < NGRP; ++q) {
-#pragma unroll
-      for (int c = 0; c < GRP; ++c) {
-        if ((keep >> (q * GRP + c)) & 1u)
-          base[slot++] = pack(f2key(__float_as_uint(val[q * GRP + c])), ebase + q * 64 * GRP + c);
-      }
-    }
-  }
-  if (lane == 0) {
-    WaveRec r;
-    r.maxp = wmax;
-    r.mass = wmass;
-    r.mref = m_ref;
-    r.count = run <= (uint32_t)WCAP ? run : RESCAN;
-    r.th1 = th1;
-    r.flags = wflags;
-    A.wave_rec[((int64_t)row * S + seg) * NWS + wave] = r;
-  }
-}
-
-// ---------------------------------------------------------------------------
 // Descending bitonic sort of n <= CAP packed candidates held in LDS `a`.
 // Element i = r * NT + tid lives in register v[r] of its thread. A
 // compare-exchange stage with partner distance j runs through wave shuffles
@@ -986,212 +747,463 @@ __device__ void sort_desc_small(uint64_t* a, uint64_t* b, int n) {
 // ---------------------------------------------------------------------------
 // smp_finish: one block per row.
 // ---------------------------------------------------------------------------
-template <int DT, bool PEN>
-__global__ __launch_bounds__(NT) void smp_finish(SmpArgs A) {
-  __shared__ FinishLds fl;
-  __shared__ uint64_t red_u64[NW];
-  __shared__ double red_f64[NW];
-  __shared__ int red_int[NW];
-  __shared__ uint32_t red_u32[NW];
-  __shared__ uint32_t bc[4];
-  __shared__ TailShared ts;
+struct RowLds {
+  uint64_t buf[BUFCAP];    // append buffer of candidates (unordered)
+  uint64_t cand[CAP];      // the candidates that pass the final bounds, sorted
+  double w[CAP];           // weights of the tail; scratch of the sorts
+  uint32_t lists[NW * KBMAX];  // the waves' top-KB lists, merged after the stream
+  uint2 def[DEFCAP];           // deferred chunks: (chunk, its largest key)
+};
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int row = blockIdx.x;
-  const int32_t V = A.V;
-  const int W = A.S * NWS;
-  const DevParams P = A.prm[A.prm_shared ? 0 : row];
-  const RowPlan plan = make_plan(A, P);
-  uint32_t pflags = 0;
-  const RowCtx rc = make_rowctx<PEN>(A, P, row, DT == 0 ? 4 : 2, &pflags);
-  const WaveRec* recs = A.wave_rec + (int64_t)row * W;
-
-  // ---- wave records: row max, top-KB threshold, flags, counts -----------
-  uint64_t rmax = 0, rkb = 0;
-  uint32_t rflags = pflags;
-  for (int w = tid; w < W; w += NT) {
-    const WaveRec r = recs[w];
-    rmax = r.maxp > rmax ? r.maxp : rmax;
-    rkb = r.th1 > rkb ? r.th1 : rkb;
-    rflags |= r.flags;
-    fl.cnt[w] = r.count == RESCAN ? 0u : r.count;
-    fl.res[w] = r.count == RESCAN ? 1u : 0u;
-  }
-  rmax = block_max_u64(rmax, red_u64);
-  rkb = block_max_u64(rkb, red_u64);
-  {
-    // OR of the flags across the block: every decision below (status, dense
-    // or compact) must be uniform over the block's threads
-    uint32_t f = rflags;
+// Raw bits of chunk c (2,048 logits) of a row into kb; nothing for c >= nch.
+// Element (q, j) of this lane is eb + q * 64 * GRP + j.
+template <int DT, bool VEC>
+__device__ __forceinline__ void load_chunk(const RowCtx& rc, int32_t V, int nch, int c, int lane,
+                                           uint32_t (&kb)[EPT]) {
+  constexpr int GRP = (DT == 0) ? 4 : 8;
+  constexpr int NGRP = EPT / GRP;
+  if (c >= nch) return;
+  const uint32_t w0 = (uint32_t)c * WSEG;
+  const uint32_t eb = w0 + (uint32_t)lane * GRP;
+  if (VEC && w0 + WSEG <= (uint32_t)V) {
+    const uint4* src = (const uint4*)(rc.base + (size_t)eb * (DT == 0 ? 4 : 2));
 #pragma unroll
-    for (int o = 32; o > 0; o >>= 1) f |= __shfl_xor(f, o);
-    __syncthreads();
-    if (lane == 0) red_u32[wave] = f;
-    __syncthreads();
-    f = 0;
-#pragma unroll
-    for (int w = 0; w < NW; ++w) f |= red_u32[w];
-    rflags = f;
-  }
-  // exclusive scans of the counts and of the re-scan flags; thread t owns
-  // the four records 4t .. 4t+3 (W <= MAX_WAVES = 4 * NT)
-  int csum = 0, nres = 0;
-  {
-    uint32_t c4[4], r4[4];
-    int sc = 0, sr = 0;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int w = 4 * tid + i;
-      c4[i] = w < W ? fl.cnt[w] : 0u;
-      r4[i] = w < W ? fl.res[w] : 0u;
-      sc += (int)c4[i];
-      sr += (int)r4[i];
+    for (int q = 0; q < NGRP; ++q) {
+      const uint4 v = src[q * 64];
+      if (DT == 0) {
+        kb[q * 4 + 0] = v.x;
+        kb[q * 4 + 1] = v.y;
+        kb[q * 4 + 2] = v.z;
+        kb[q * 4 + 3] = v.w;
+      } else {
+        kb[q * 8 + 0] = v.x << 16;
+        kb[q * 8 + 1] = v.x & 0xffff0000u;
+        kb[q * 8 + 2] = v.y << 16;
+        kb[q * 8 + 3] = v.y & 0xffff0000u;
+        kb[q * 8 + 4] = v.z << 16;
+        kb[q * 8 + 5] = v.z & 0xffff0000u;
+        kb[q * 8 + 6] = v.w << 16;
+        kb[q * 8 + 7] = v.w & 0xffff0000u;
+      }
     }
-    const int exc = block_excl_scan(sc, red_int, &csum);
-    const int exr = block_excl_scan(sr, red_int, &nres);
-    __syncthreads();  // every read of fl.res above precedes the list writes
-    int oc = exc, orr = exr;
+  } else {
+    // offsets o of this lane lie inside the row iff o < lim (compared
+    // against immediates: no per-element index registers)
+    const int32_t lim = V - (int32_t)eb;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int w = 4 * tid + i;
-      if (w < W) {
-        fl.off[w] = (uint32_t)oc;
-        oc += (int)c4[i];
-        if (r4[i]) fl.res[orr++] = (uint32_t)w;
+    for (int q = 0; q < NGRP; ++q) {
+#pragma unroll
+      for (int j = 0; j < GRP; ++j) {
+        const int32_t o = q * 64 * GRP + j;
+        kb[q * GRP + j] = o < lim ? raw_bits<DT>(rc, eb + (uint32_t)o) : 0u;
       }
     }
   }
-  const float M = key2f(pk_key(rmax));
+}
+
+// Chunk c's raw bits -> binary32 value bits in place (penalties applied,
+// absent elements -inf); non-finite test and lane maximum.
+template <int DT, bool PEN>
+__device__ __forceinline__ void chunk_values(const RowCtx& rc, int32_t V, int c, int lane,
+                                             uint32_t (&kb)[EPT], float& lmax, bool& bad) {
+  constexpr int GRP = (DT == 0) ? 4 : 8;
+  constexpr int NGRP = EPT / GRP;
+  const uint32_t w0 = (uint32_t)c * WSEG;
+  const uint32_t eb = w0 + (uint32_t)lane * GRP;
+  const bool full = w0 + WSEG <= (uint32_t)V;
+  const int32_t lim = V - (int32_t)eb;
+#pragma unroll
+  for (int q = 0; q < NGRP; ++q) {
+    uint32_t wbits = 0;
+    if (PEN && rc.bitmap && q * 64 * GRP < lim) wbits = rc.bitmap[(eb + q * 64 * GRP) >> 5];
+#pragma unroll
+    for (int j = 0; j < GRP; ++j) {
+      const int32_t o = q * 64 * GRP + j;
+      uint32_t b = kb[q * GRP + j];
+      float v = -__builtin_inff();
+      if (full || o < lim) {
+        if (PEN && rc.bitmap && ((wbits >> ((eb + o) & 31)) & 1u)) {
+          const uint32_t e = eb + (uint32_t)o;
+          b = penalize(b, pen_count(rc, e), rc);
+        }
+        v = __uint_as_float(b);
+        bad |= __builtin_amdgcn_class(v, 0x207) != 0;  // signaling/quiet NaN, +-inf
+      }
+      kb[q * GRP + j] = __float_as_uint(v);
+      lmax = fmaxf(lmax, v);
+    }
+  }
+}
+
+// Per-wave streaming state.
+struct WaveState {
+  uint32_t wkey;  // largest key this wave has seen (uniform)
+  float m_ref;    // reference point of the wave's logprob mass (uniform)
+  double acc;     // per lane: sum of exp(l - m_ref) over l >= m_ref - ZMASS
+  bool bad;       // per lane: a non-finite value was seen
+};
+
+// Shared streaming state of a row block.
+struct RowShared {
+  uint32_t count;   // entries appended (beyond BUFCAP they went to the spill area)
+  uint32_t mkey;    // running row maximum key
+  uint32_t flags;   // F_* of the row
+  uint32_t theta;   // best top-KB bound any wave has certified
+  uint32_t q[NW];   // per wave: the ceil(KB/8)-th value of its list
+  uint32_t ndef;    // deferred chunks recorded (may exceed DEFCAP: those were not deferred)
+  uint32_t ctr;     // compaction counter
+};
+
+// Wave maximum of the chunk just converted; the row maximum in LDS follows.
+__device__ __forceinline__ void chunk_max(float lmax, WaveState& ws, RowShared& sh) {
+  const uint32_t lk = lmax == -__builtin_inff() ? 0u : f2key(__float_as_uint(lmax));
+  const uint32_t wm = wave_max_dpp(lk);
+  if (wm > ws.wkey) {
+    ws.wkey = wm;
+    if ((threadIdx.x & 63) == 0) atomicMax(&sh.mkey, wm);
+  }
+}
+
+// Mass terms (if mass) and candidates of chunk c for threshold thr. The
+// chunk's survivors are counted first and their slots reserved with one LDS
+// atomic; then only element slots where some lane holds a value >=
+// min(threshold, m_ref - ZMASS) do any work. Mass terms are binary32
+// exponentials accumulated in binary64: next to the row maximum's term (1.0)
+// the small terms must not be rounded away, since the top token's logprob is
+// -log(1 + their sum). Slots beyond BUFCAP go to the row's spill area in
+// global memory (each element is appended at most once, so V entries always
+// suffice); that rare path ends with a full wait, so the common path holds
+// only LDS stores and the compiler can keep the prefetched chunk in flight.
+template <int DT>
+__device__ __forceinline__ void chunk_filter(int c, int lane, const uint32_t (&kb)[EPT], uint32_t thr,
+                                             uint32_t mk, bool mass, uint32_t cmax, bool may_defer,
+                                             WaveState& ws, RowShared& sh, RowLds& fl, uint64_t* spill) {
+  constexpr int GRP = (DT == 0) ? 4 : 8;
+  if (mk == 0u) return;  // nothing finite seen yet: the row is rejected anyway
+  const float thf = key_threshold_float(thr);
+  float lo = __builtin_inff();
+  if (mass) {
+    const float Mt = key2f(mk);
+    if (Mt > ws.m_ref) {
+      if (ws.m_ref != -__builtin_inff()) ws.acc *= exp((double)ws.m_ref - (double)Mt);
+      ws.m_ref = Mt;
+    }
+    lo = ws.m_ref - ZMASS;
+  }
+  // nothing in the chunk reaches the lower of the two cuts: no work at all
+  if (!(key2f(cmax) >= fminf(thf, lo))) return;
+  const uint32_t eb = (uint32_t)c * WSEG + (uint32_t)lane * GRP;
+  uint32_t cnt = 0;
+#pragma unroll
+  for (int i = 0; i < EPT; ++i) cnt += (uint32_t)__popcll(__ballot(__uint_as_float(kb[i]) >= thf));
+  // A chunk with many survivors (the running bounds are still low) is
+  // deferred: recorded with its largest key and read again at the end, and
+  // only if that key reaches the final bound.
+  if (may_defer && cnt > (uint32_t)DCHUNK) {
+    uint32_t idx = 0;
+    if (lane == 0) idx = atomicAdd(&sh.ndef, 1u);
+    idx = (uint32_t)__builtin_amdgcn_readfirstlane((int)idx);
+    if (idx < (uint32_t)DEFCAP) {
+      if (lane == 0) fl.def[idx] = make_uint2((uint32_t)c, cmax);
+      cnt = 0;
+    }
+  }
+  uint32_t base = 0;
+  if (cnt) {
+    if (lane == 0) base = atomicAdd(&sh.count, cnt);
+    base = (uint32_t)__builtin_amdgcn_readfirstlane((int)base);
+  }
+  const bool spill_now = base + cnt > (uint32_t)BUFCAP;
+  const bool skip = cnt == 0u;
+  const float tany = (spill_now || skip) ? lo : fminf(thf, lo);
+  uint32_t off = base;
+#pragma unroll
+  for (int i = 0; i < EPT; ++i) {
+    const float v = __uint_as_float(kb[i]);
+    if (__ballot(v >= tany)) {
+      if (v >= lo) ws.acc += (double)__builtin_amdgcn_exp2f((v - ws.m_ref) * 1.4426950408889634f);
+      if (!spill_now && !skip) {
+        const bool k = v >= thf;
+        const uint64_t km = __ballot(k);
+        if (k)
+          fl.buf[off + lanes_below(km)] =
+              pack(f2key(__float_as_uint(v)), eb + (uint32_t)((i / GRP) * 64 * GRP + (i % GRP)));
+        off += (uint32_t)__popcll(km);
+      }
+    }
+  }
+  if (spill_now) {
+    // rare: the buffer is full. Slots below BUFCAP to LDS, the rest to the
+    // spill area, in separate loops (never one store to either space)
+    off = base;
+#pragma unroll
+    for (int i = 0; i < EPT; ++i) {
+      const float v = __uint_as_float(kb[i]);
+      const bool k = v >= thf;
+      const uint64_t km = __ballot(k);
+      const uint32_t slot = off + lanes_below(km);
+      if (k && slot < (uint32_t)BUFCAP)
+        fl.buf[slot] = pack(f2key(__float_as_uint(v)), eb + (uint32_t)((i / GRP) * 64 * GRP + (i % GRP)));
+      off += (uint32_t)__popcll(km);
+    }
+    off = base;
+#pragma unroll
+    for (int i = 0; i < EPT; ++i) {
+      const float v = __uint_as_float(kb[i]);
+      const bool k = v >= thf;
+      const uint64_t km = __ballot(k);
+      const uint32_t slot = off + lanes_below(km);
+      if (k && slot >= (uint32_t)BUFCAP)
+        __builtin_nontemporal_store(
+            pack(f2key(__float_as_uint(v)), eb + (uint32_t)((i / GRP) * 64 * GRP + (i % GRP))),
+            &spill[slot - BUFCAP]);
+      off += (uint32_t)__popcll(km);
+    }
+    __builtin_amdgcn_s_waitcnt(0);
+  }
+}
+
+// Order-free parallel compaction: appends to dst the entries of src[0, n)
+// with key >= thr, at most cap in all; *ctr counts every qualifying entry
+// (reset first if `reset`). Returns *ctr (every thread). Block-wide.
+__device__ __forceinline__ uint32_t compact_entries(const uint64_t* src, uint32_t n, uint64_t* dst,
+                                                    uint32_t cap, uint32_t thr, uint32_t* ctr, bool reset) {
+  const int tid = threadIdx.x, lane = tid & 63;
+  if (reset) {
+    __syncthreads();
+    if (tid == 0) *ctr = 0u;
+  }
+  __syncthreads();
+  for (uint32_t i0 = 0; i0 < n; i0 += NT) {
+    const uint32_t i = i0 + (uint32_t)tid;
+    uint64_t e = 0;
+    bool keep = false;
+    if (i < n) {
+      e = src[i];
+      keep = pk_key(e) >= thr;
+    }
+    const uint64_t m = __ballot(keep);
+    if (m) {
+      const int first = (int)__builtin_ctzll(m);
+      uint32_t base = 0;
+      if (lane == first) base = atomicAdd(ctr, (uint32_t)__popcll(m));
+      base = (uint32_t)__builtin_amdgcn_readlane((int)base, first);
+      const uint32_t slot = base + lanes_below(m);
+      if (keep && slot < cap) dst[slot] = e;
+    }
+  }
+  __syncthreads();
+  const uint32_t r = *ctr;
+  __syncthreads();
+  return r;
+}
+
+// ---------------------------------------------------------------------------
+// smp_row: one block of 8 wave64s per row, streaming the whole row.
+//
+// The row is read in rounds: in round k wave w takes chunk 8k + w (2,048
+// logits, 32 values per lane, coalesced 16-byte loads), with the chunk of
+// round k + 1 already in flight. One barrier per round publishes the waves'
+// maxima; every wave then filters its chunk with the row's bounds as they
+// stand and appends the elements that can matter to an LDS buffer. After the
+// last round the same block sorts the candidates and runs the reference's
+// truncation and draw: no second launch, no traffic between blocks.
+// ---------------------------------------------------------------------------
+template <int DT, bool VEC, bool PEN>
+__global__ __launch_bounds__(NT) void smp_row(SmpArgs A) {
+  __shared__ RowLds fl;
+  __shared__ RowShared sh;
+  __shared__ uint64_t red_u64[NW];
+  __shared__ double red_f64[NW];
+  __shared__ int red_int[NW];
+  __shared__ float s_mref[NW];
+  __shared__ double s_mass[NW];
+  __shared__ TailShared ts;
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int row = blockIdx.x;
+  const int32_t V = A.V;
+  const DevParams P = A.prm[A.prm_shared ? 0 : row];
+  const RowPlan plan = make_plan(A, P);
+  uint32_t wflags = 0;
+  const RowCtx rc = make_rowctx<PEN>(A, P, row, DT == 0 ? 4 : 2, &wflags);
+  const int nch = (V + WSEG - 1) / WSEG;
+  if (tid == 0) {
+    sh.count = 0u;
+    sh.mkey = 0u;
+    sh.flags = 0u;
+    sh.theta = 0u;
+    sh.ndef = 0u;
+  }
+  if (tid < NW) {
+    sh.q[tid] = 0u;
+  }
+  uint64_t* const spill = A.dense_b + (int64_t)row * A.dense_ld;
+
+  WaveState ws;
+  ws.wkey = 0u;
+  ws.m_ref = -__builtin_inff();
+  ws.acc = 0.0;
+  ws.bad = false;
+  uint32_t buf0[EPT], buf1[EPT];
+  load_chunk<DT, VEC>(rc, V, nch, wave, lane, buf0);
+  load_chunk<DT, VEC>(rc, V, nch, wave + NW, lane, buf1);
+  __builtin_amdgcn_sched_barrier(0);  // both chunks in flight before any work
+  __syncthreads();  // shared state initialised
+
+  // Each wave keeps the KB largest lane maxima of its chunks so far, sorted
+  // descending in lanes 0..KB-1 (distinct elements: KB of them are at or
+  // above the list's last value, which is therefore a valid top-KB bound).
+  // Waves share the best such bound and the row maximum through LDS atomics;
+  // nothing in the stream waits for another wave.
+  uint32_t lst = 0u, theta_w = 0u, q_pub = 0u;
+  const int qidx = (plan.KB + NW - 1) / NW - 1;
+  // per chunk: its r largest lane maxima enter the list (the first chunk: up
+  // to KB of them, so the bound exists from the start)
+  const int r_first = plan.KB < 64 ? plan.KB : 64;
+  const int r_next = plan.KB < 8 ? plan.KB : 8;
+
+  // one chunk: c from X; prefetch the wave's chunk two steps ahead into X
+  auto step = [&](uint32_t (&X)[EPT], int c, bool first) {
+    float lmax = -__builtin_inff();
+    chunk_values<DT, PEN>(rc, V, c, lane, X, lmax, ws.bad);
+    uint32_t lk = lmax == -__builtin_inff() ? 0u : f2key(__float_as_uint(lmax));
+    uint32_t cmax = 0u;
+    const int rr = first ? r_first : r_next;
+    for (int i = 0; i < rr; ++i) {
+      const uint32_t m = wave_max_dpp(lk);
+      if (i == 0) cmax = m;
+      if (m <= theta_w) break;  // 0, or cannot enter the full list
+      // insert m: entries >= m keep their lanes, the rest move up by one
+      const uint32_t pos = (uint32_t)__popcll(__ballot(lane < plan.KB && lst >= m));
+      const uint32_t up = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)lst, 0x138, 0xf, 0xf, false);  // wave_shr:1
+      lst = (uint32_t)lane < pos ? lst : ((uint32_t)lane == pos ? m : up);
+      theta_w = (uint32_t)__builtin_amdgcn_readlane((int)lst, plan.KB - 1);
+      const uint64_t eq = __ballot(lk == m);
+      if (lane == (int)__builtin_ctzll(eq)) lk = 0u;
+    }
+    if (cmax > ws.wkey) {
+      ws.wkey = cmax;
+      if (lane == 0) atomicMax(&sh.mkey, cmax);
+    }
+    // Two certified bounds: the best single wave's KB-th value, and the
+    // minimum over the waves of their ceil(KB/8)-th values (each wave has
+    // that many elements at or above it: 8 * ceil(KB/8) >= KB in all).
+    uint32_t th = (uint32_t)__builtin_amdgcn_readfirstlane(
+        __hip_atomic_load(&sh.theta, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP));
+    if (theta_w > th) {
+      if (lane == 0) atomicMax(&sh.theta, theta_w);
+      th = theta_w;
+    }
+    {
+      const uint32_t qw = (uint32_t)__builtin_amdgcn_readlane((int)lst, qidx);
+      if (qw > q_pub) {
+        q_pub = qw;
+        if (lane == 0) __hip_atomic_store(&sh.q[wave], qw, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+      }
+      uint32_t qmin = lane < NW ? __hip_atomic_load(&sh.q[lane], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP)
+                                : 0xffffffffu;
+      qmin = (uint32_t)__builtin_amdgcn_readfirstlane((int)wave_min_u32_dpp(qmin));
+      th = qmin > th ? qmin : th;
+    }
+    // the row maximum as LDS holds it (a workgroup-scope atomic read: a
+    // volatile access through a generic pointer would become a flat load
+    // that waits for every outstanding global load -- the prefetch)
+    uint32_t mk = (uint32_t)__builtin_amdgcn_readfirstlane(
+        __hip_atomic_load(&sh.mkey, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP));
+    mk = mk > ws.wkey ? mk : ws.wkey;
+    const uint32_t thr = A.force_dense ? 0xffffffffu : row_threshold(plan, P, key2f(mk), th);
+    chunk_filter<DT>(c, lane, X, thr, mk, A.want_mass != 0, cmax, true, ws, sh, fl, spill);
+    load_chunk<DT, VEC>(rc, V, nch, c + 2 * NW, lane, X);
+  };
+  for (int c = wave; c < nch; c += 2 * NW) {
+    step(buf0, c, c == wave);
+    if (c + NW < nch) step(buf1, c + NW, false);
+  }
+  // the exact bound of the union of the waves' lists (8 * KB distinct
+  // elements): the KB-th largest of them
+  if (lane < plan.KB) fl.lists[wave * plan.KB + lane] = lst;
+  __syncthreads();  // every append, deferral, list and maximum is in LDS
+  {
+    const int nl = NW * plan.KB;
+    for (int t = tid; t < nl; t += NT) {
+      const uint32_t x = fl.lists[t];
+      if (x != 0u) {
+        int rank = 0;
+        for (int j = 0; j < nl; ++j) {
+          const uint32_t y = fl.lists[j];
+          rank += (y > x || (y == x && j < t)) ? 1 : 0;
+        }
+        if (rank == plan.KB - 1) atomicMax(&sh.theta, x);
+      }
+    }
+  }
+  __syncthreads();
+  const uint32_t theta = sh.theta;
+  // deferred chunks whose largest key reaches the final bound: read again
+  // and filter with that bound (the wave with the entry's index mod NW)
+  if (!A.force_dense) {
+    const uint32_t mkf = sh.mkey;
+    const uint32_t thr_f = row_threshold(plan, P, key2f(mkf), theta);
+    const uint32_t nd = sh.ndef < (uint32_t)DEFCAP ? sh.ndef : (uint32_t)DEFCAP;
+    for (uint32_t i = (uint32_t)wave; i < nd; i += NW) {
+      const uint2 d = fl.def[i];
+      if (d.y >= thr_f) {
+        uint32_t kb[EPT];
+        load_chunk<DT, VEC>(rc, V, nch, (int)d.x, lane, kb);
+        float lmax = -__builtin_inff();
+        bool bad = false;
+        chunk_values<DT, PEN>(rc, V, (int)d.x, lane, kb, lmax, bad);
+        chunk_filter<DT>((int)d.x, lane, kb, thr_f, mkf, false, d.y, false, ws, sh, fl, spill);
+      }
+    }
+  }
+  if (__ballot(ws.bad)) wflags |= F_NONFINITE;
+  {
+    const double wm = A.want_mass ? wave_sum_f64(ws.acc) : 0.0;
+    if (lane == 0) {
+      if (wflags) atomicOr(&sh.flags, wflags);
+      s_mref[wave] = ws.m_ref;
+      s_mass[wave] = wm;
+    }
+  }
+  __syncthreads();
+
+  // ---- row results -----------------------------------------------------
+  const float M = key2f(sh.mkey);
+  const uint32_t rflags = sh.flags;
   double logZ = 0.0;
   if (A.want_mass) {
     double part = 0.0;
-    for (int w = tid; w < W; w += NT) {
-      const WaveRec r = recs[w];
-      if (r.maxp) part += r.mass * exp((double)r.mref - (double)M);
-    }
-    logZ = log(block_sum_f64(part, red_f64));
+#pragma unroll
+    for (int w = 0; w < NW; ++w)
+      if (s_mref[w] != -__builtin_inff()) part += s_mass[w] * exp((double)s_mref[w] - (double)M);
+    logZ = log(part);
   }
   int32_t status = ST_OK;
   if (rflags & F_INVALID) status = ST_EINVAL;
   else if (rflags & F_NONFINITE) status = ST_ENONFINITE;
 
   if (status == ST_OK) {
-    // Final threshold from exact row quantities: every wave filtered with
-    // bounds no larger than these, so the survivors gathered below are
-    // exactly the row's elements with key >= theta_f, whatever the timing.
-    // Row-wide top-KB bound from the lane maxima the scan blocks published
-    // (distinct elements of this row, all written by this call): the KB-th
-    // largest of them has at least KB elements at or above it. At most 512
-    // are used: the `per` largest of each block.
-    uint32_t theta_pub = 0u;
-    {
-      const int S = A.S;
-      const int per = S * TOPS <= NT ? TOPS : (NT / S > 0 ? NT / S : 1);
-      const int npub = per * S < NT ? per * S : NT;
-      uint32_t* pub = (uint32_t*)fl.w;
-      if (tid == 0) bc[1] = 0u;
-      if (tid < npub) {
-        const int sg = tid / per, k = tid - sg * per;
-        pub[tid] = A.tops[((int64_t)row * MAX_SEGMENTS + sg) * TOPS + (TOPS - 1 - k)];
-      }
-      __syncthreads();
-      if (tid < npub) {
-        const uint32_t x = pub[tid];
-        if (x != 0u) {
-          int rank = 0;
-#pragma unroll 16
-          for (int i = 0; i < npub; ++i) {
-            const uint32_t y = pub[i];
-            rank += (y > x || (y == x && i < tid)) ? 1 : 0;
-          }
-          if (rank == plan.KB - 1) bc[1] = x;
-        }
-      }
-      __syncthreads();
-      theta_pub = bc[1];
-    }
-    const uint32_t theta_f =
-        row_threshold(plan, P, M, (uint32_t)rkb > theta_pub ? (uint32_t)rkb : theta_pub);
+    // Every element with key >= theta_f = row_threshold(M, theta) was
+    // appended (every bound used was no larger), so the appended entries at
+    // or above theta_f are exactly the row's: sorted, they hold the top-KB
+    // and every relevant element, which is all the outputs and the tail read.
+    const uint32_t theta_f = row_threshold(plan, P, M, theta);
     bool dense = A.force_dense != 0;
-    const uint64_t* cand;
-    double* wbuf;
     int64_t ncand = 0;
     if (!dense) {
-      if (tid == 0) bc[0] = 0u;
-      __syncthreads();
-      const uint64_t* wc = A.wave_cand + (int64_t)row * W * WCAP;
-      // (a) candidates handed over by the waves
-      for (int i0 = 0; i0 < csum; i0 += NT) {
-        const int idx = i0 + tid;
-        bool keep = false;
-        uint64_t p = 0;
-        if (idx < csum) {
-          int lo = 0, hi = W - 1;  // largest w with off[w] <= idx
-          while (lo < hi) {
-            const int mid = (lo + hi + 1) >> 1;
-            if ((int)fl.off[mid] <= idx) lo = mid; else hi = mid - 1;
-          }
-          p = wc[(int64_t)lo * WCAP + (idx - (int)fl.off[lo])];
-          keep = pk_key(p) >= theta_f;
-        }
-        const uint64_t m = __ballot(keep);
-        uint32_t base = 0;
-        if (lane == 0 && m) base = atomicAdd(&bc[0], (uint32_t)__popcll(m));
-        base = __shfl(base, 0);
-        const uint32_t slot = base + (uint32_t)__popcll(m & ((lane == 0) ? 0ull : (~0ull >> (64 - lane))));
-        if (keep && slot < (uint32_t)CAP) fl.cand[slot] = p;
-      }
-      // (b) waves that handed over nothing: read their logits again, four
-      // consecutive elements per thread (one 16-byte or 8-byte load when the
-      // rows are aligned), two groups per iteration
-      const int64_t ngrp = (int64_t)nres * (WSEG / 4);
-      for (int64_t t0 = 0; t0 < ngrp; t0 += 2 * NT) {
-        uint32_t kk[2][4];
-        int64_t e0[2];
-#pragma unroll
-        for (int h = 0; h < 2; ++h) {
-          const int64_t t = t0 + h * NT + tid;
-          e0[h] = 0;
-#pragma unroll
-          for (int c = 0; c < 4; ++c) kk[h][c] = 0u;
-          if (t < ngrp) {
-            e0[h] = (int64_t)fl.res[t / (WSEG / 4)] * WSEG + (t % (WSEG / 4)) * 4;
-            if (!PEN && A.vec && e0[h] + 4 <= V) {
-              uint32_t b[4];
-              if (DT == 0) {
-                const uint4 q = *(const uint4*)(rc.base + e0[h] * 4);
-                b[0] = q.x; b[1] = q.y; b[2] = q.z; b[3] = q.w;
-              } else {
-                const uint2 q = *(const uint2*)(rc.base + e0[h] * 2);
-                b[0] = q.x << 16; b[1] = q.x & 0xffff0000u; b[2] = q.y << 16; b[3] = q.y & 0xffff0000u;
-              }
-#pragma unroll
-              for (int c = 0; c < 4; ++c) kk[h][c] = f2key(b[c]);
-            } else {
-#pragma unroll
-              for (int c = 0; c < 4; ++c)
-                kk[h][c] = (e0[h] + c < V) ? f2key(value_bits<DT, PEN>(rc, e0[h] + c)) : 0u;
-            }
-          }
-        }
-#pragma unroll
-        for (int h = 0; h < 2; ++h) {
-#pragma unroll
-          for (int c = 0; c < 4; ++c) {
-            const bool keep = kk[h][c] >= theta_f;
-            const uint64_t m = __ballot(keep);
-            uint32_t base = 0;
-            if (lane == 0 && m) base = atomicAdd(&bc[0], (uint32_t)__popcll(m));
-            base = __shfl(base, 0);
-            const uint32_t slot = base + (uint32_t)__popcll(m & ((lane == 0) ? 0ull : (~0ull >> (64 - lane))));
-            if (keep && slot < (uint32_t)CAP) fl.cand[slot] = pack(kk[h][c], (uint32_t)(e0[h] + c));
-          }
-        }
-      }
-      __syncthreads();
-      ncand = (int64_t)bc[0];
-      if (ncand > CAP || ncand < 1) dense = true;
+      const uint32_t cnt = sh.count;
+      const uint32_t n = cnt < (uint32_t)BUFCAP ? cnt : (uint32_t)BUFCAP;
+      uint32_t nc = compact_entries(fl.buf, n, fl.cand, CAP, theta_f, &sh.ctr, true);
+      if (cnt > (uint32_t)BUFCAP)
+        nc = compact_entries(spill, cnt - (uint32_t)BUFCAP, fl.cand, CAP, theta_f, &sh.ctr, false);
+      ncand = (int64_t)nc;
+      dense = ncand > CAP || ncand < 1;
     }
+    const uint64_t* cand;
+    double* wbuf;
     if (!dense) {
       if (ncand <= NT) sort_desc_small(fl.cand, (uint64_t*)fl.w, (int)ncand);
       else sort_desc(fl.cand, (int)ncand);
@@ -1206,8 +1218,13 @@ __global__ __launch_bounds__(NT) void smp_finish(SmpArgs A) {
       wbuf = A.dense_w + (int64_t)row * A.dense_ld;
     }
 
+    __syncthreads();  // the sorted candidates are visible to every thread
+    // The row maximum is always a candidate: cand[0] is the argmax (larger
+    // value, then smaller id).
+    const uint32_t amax = pk_id(cand[0]);
+
     // ---- outputs in raw order ------------------------------------------
-    if (A.argmax && tid == 0) A.argmax[row] = pk_id(rmax);
+    if (A.argmax && tid == 0) A.argmax[row] = amax;
     if (A.top8_ids) {
       for (int i = tid; i < 8; i += NT) {
         const bool in = i < ncand;
@@ -1260,7 +1277,7 @@ __global__ __launch_bounds__(NT) void smp_finish(SmpArgs A) {
     if (A.out_ids) {
       if (P.greedy) {
         const int nd = A.mode == MODE_VERIFY ? 1 : A.n_draws;
-        for (int d = tid; d < nd; d += NT) A.out_ids[(int64_t)row * A.n_draws + d] = pk_id(rmax);
+        for (int d = tid; d < nd; d += NT) A.out_ids[(int64_t)row * A.n_draws + d] = amax;
       } else {
         int64_t c;
         if (plan.need_rel) {
@@ -1278,7 +1295,6 @@ __global__ __launch_bounds__(NT) void smp_finish(SmpArgs A) {
     if (tid == 0 && A.stats) {
       atomicAdd(&A.stats[STAT_ROWS], 1ull);
       if (dense) atomicAdd(&A.stats[STAT_DENSE_ROWS], 1ull);
-      atomicAdd(&A.stats[STAT_RESCAN_WAVES], (unsigned long long)nres);
       atomicAdd(&A.stats[STAT_CANDIDATES], (unsigned long long)ncand);
     }
   } else if (A.out_ids) {
@@ -1289,8 +1305,6 @@ __global__ __launch_bounds__(NT) void smp_finish(SmpArgs A) {
     A.status[row] = status;
     if (A.row_status) A.row_status[row] = status;
   }
-  // clear the row's bound slots for the next call (ordered by the kernel boundary)
-  for (int sg = tid; sg < A.S; sg += NT) A.slots[(int64_t)row * MAX_SEGMENTS + sg] = 0ull;
 
   // ---- verify: the last finished row applies the acceptance rule --------
   if (A.mode == MODE_VERIFY) {
@@ -1420,10 +1434,7 @@ __global__ __launch_bounds__(1024) void smp_penalty_prep(PenArgs A) {
 // ---------------------------------------------------------------------------
 template <int DT, bool VEC, bool PEN>
 static hipError_t launch_t(const SmpArgs& a, hipStream_t st) {
-  hipLaunchKernelGGL((smp_scan<DT, VEC, PEN>), dim3((unsigned)(a.S * a.rows)), dim3(NTS), 0, st, a);
-  hipError_t e = hipGetLastError();
-  if (e != hipSuccess) return e;
-  hipLaunchKernelGGL((smp_finish<DT, PEN>), dim3((unsigned)a.rows), dim3(NT), 0, st, a);
+  hipLaunchKernelGGL((smp_row<DT, VEC, PEN>), dim3((unsigned)a.rows), dim3(NT), 0, st, a);
   return hipGetLastError();
 }
 
