@@ -15,7 +15,7 @@ constexpr int EPT = 32;            // elements per lane per chunk
 constexpr int WSEG = 64 * EPT;     // elements per chunk
 constexpr int CAP = 4096;          // candidates a row block sorts in LDS
 constexpr int BUFCAP = 8192;       // candidates a row block's append buffer holds
-constexpr int DCHUNK = 64;         // survivors above which a chunk is deferred
+constexpr int DLANES = 16;         // lanes with survivors above which a chunk is deferred
 constexpr int DEFCAP = 1024;       // deferred chunks a row block records
 constexpr int KBMAX = 64;          // largest "small" top-k / list length
 constexpr int HCAP = 16384;        // history tokens per row for the penalties

@@ -454,6 +454,85 @@ __device__ __forceinline__ void sample_tail(const SmpArgs& A, const DevParams& P
 }
 
 // ---------------------------------------------------------------------------
+// The same truncation and draw by one wave, for one draw over c <= 64
+// sorted candidates (the common case): candidate j in lane j; weights and
+// scores in one parallel pass; the reference's serial binary64 sums run in
+// candidate order over values broadcast from the lanes (readlane).
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ double lane_f64(double x, int j) {
+  const uint64_t b = (uint64_t)__double_as_longlong(x);
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)b, j);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(b >> 32), j);
+  return __longlong_as_double((long long)(((uint64_t)hi << 32) | lo));
+}
+
+__device__ __forceinline__ void sample_tail_wave(const SmpArgs& A, const DevParams& P, int row,
+                                                 const uint64_t* cand, int c) {
+  const int lane = threadIdx.x & 63;
+  const double T = P.temperature;
+  const float v0 = key2f(pk_key(cand[0]));
+  const uint64_t pos = position_of(A, row, 0);
+  const bool in = lane < c;
+  const uint64_t cj = in ? cand[lane] : 0ull;
+  double z = 0.0, w = 0.0, sc = -__builtin_inf();
+  if (in) {
+    z = ((double)key2f(pk_key(cj)) - (double)v0) / T;  // widen, subtract, divide
+    w = exp_d(z);
+    if (P.version == YSKN_V3) sc = z + gumbel_from_key(position_key(P.seed, pos), pk_id(cj));
+  }
+  // top-p: first n with prefix >= top_p * total (serial sums in candidate order)
+  double total = 0.0;
+  for (int j = 0; j < c; ++j) total = total + lane_f64(w, j);
+  const double thr = P.top_p * total;
+  int n = c;
+  double prefix = 0.0;
+  for (int j = 0; j < c; ++j) {
+    prefix = prefix + lane_f64(w, j);
+    if (prefix >= thr) {
+      n = j + 1;
+      break;
+    }
+  }
+  // min-p relative to w_0 = 1
+  if (P.min_p > 0.0) {
+    int m = 1;
+    while (m < n && lane_f64(w, m) >= P.min_p) ++m;
+    n = m;
+  }
+  int pick = n - 1;
+  if (P.version == YSKN_V3) {
+    // argmax of z + g over the retained candidates; the earliest wins ties
+    double best = lane < n ? sc : -__builtin_inf();
+    int bj = lane < n ? lane : 64;
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+      const double ob = __shfl_xor(best, o);
+      const int oj = __shfl_xor(bj, o);
+      if (ob > best || (ob == best && oj < bj)) {
+        best = ob;
+        bj = oj;
+      }
+    }
+    if (bj < n) pick = bj;
+  } else {
+    double mass = 0.0;
+    for (int j = 0; j < n; ++j) mass = mass + lane_f64(w, j);
+    const double t = uniform_v2(P.seed, pos) * mass;
+    double pre = 0.0;
+    for (int j = 0; j < n; ++j) {
+      pre = pre + lane_f64(w, j);
+      if (t < pre) {
+        pick = j;
+        break;
+      }
+    }
+  }
+  const uint32_t id = pk_id((uint64_t)(((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(cj >> 32), pick) << 32) |
+                                       (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)cj, pick)));
+  if (lane == 0) A.out_ids[(int64_t)row * A.n_draws] = id;
+}
+
+// ---------------------------------------------------------------------------
 // Dense path: exact sorted order of every element with key >= theta_D.
 // ---------------------------------------------------------------------------
 template <int DT, bool PEN>
@@ -810,6 +889,16 @@ __device__ __forceinline__ void chunk_values(const RowCtx& rc, int32_t V, int c,
   constexpr int NGRP = EPT / GRP;
   const uint32_t w0 = (uint32_t)c * WSEG;
   const uint32_t eb = w0 + (uint32_t)lane * GRP;
+  if (!PEN && w0 + WSEG <= (uint32_t)V) {
+    // a full chunk without penalties: the raw bits are the values
+#pragma unroll
+    for (int i = 0; i < EPT; ++i) {
+      const float v = __uint_as_float(kb[i]);
+      bad |= __builtin_amdgcn_class(v, 0x207) != 0;  // signaling/quiet NaN, +-inf
+      lmax = fmaxf(lmax, v);
+    }
+    return;
+  }
   const bool full = w0 + WSEG <= (uint32_t)V;
   const int32_t lim = V - (int32_t)eb;
 #pragma unroll
@@ -864,21 +953,26 @@ __device__ __forceinline__ void chunk_max(float lmax, WaveState& ws, RowShared& 
   }
 }
 
-// Mass terms (if mass) and candidates of chunk c for threshold thr. The
-// chunk's survivors are counted first and their slots reserved with one LDS
-// atomic; then only element slots where some lane holds a value >=
-// min(threshold, m_ref - ZMASS) do any work. Mass terms are binary32
+// Mass terms (if mass) and candidates of chunk c for threshold thr. Work is
+// skipped per chunk (its maximum), then per load group (GRP consecutive
+// values of a lane), then per element slot, wherever no lane holds a value
+// >= min(threshold, m_ref - ZMASS); survivors reserve their slots with one
+// LDS atomic per element slot that has any. Mass terms are binary32
 // exponentials accumulated in binary64: next to the row maximum's term (1.0)
 // the small terms must not be rounded away, since the top token's logprob is
 // -log(1 + their sum). Slots beyond BUFCAP go to the row's spill area in
 // global memory (each element is appended at most once, so V entries always
 // suffice); that rare path ends with a full wait, so the common path holds
 // only LDS stores and the compiler can keep the prefetched chunk in flight.
+// A chunk where many lanes hold survivors (the running bounds are still low)
+// is deferred instead: recorded with its largest key and read again at the
+// end, and only if that key reaches the final bound.
 template <int DT>
 __device__ __forceinline__ void chunk_filter(int c, int lane, const uint32_t (&kb)[EPT], uint32_t thr,
                                              uint32_t mk, bool mass, uint32_t cmax, bool may_defer,
                                              WaveState& ws, RowShared& sh, RowLds& fl, uint64_t* spill) {
   constexpr int GRP = (DT == 0) ? 4 : 8;
+  constexpr int NGRP = EPT / GRP;
   if (mk == 0u) return;  // nothing finite seen yet: the row is rejected anyway
   const float thf = key_threshold_float(thr);
   float lo = __builtin_inff();
@@ -890,77 +984,66 @@ __device__ __forceinline__ void chunk_filter(int c, int lane, const uint32_t (&k
     }
     lo = ws.m_ref - ZMASS;
   }
+  float tany = fminf(thf, lo);
   // nothing in the chunk reaches the lower of the two cuts: no work at all
-  if (!(key2f(cmax) >= fminf(thf, lo))) return;
-  const uint32_t eb = (uint32_t)c * WSEG + (uint32_t)lane * GRP;
-  uint32_t cnt = 0;
+  if (!(key2f(cmax) >= tany)) return;
+  float gmax[NGRP];
+  float lmax = -__builtin_inff();
 #pragma unroll
-  for (int i = 0; i < EPT; ++i) cnt += (uint32_t)__popcll(__ballot(__uint_as_float(kb[i]) >= thf));
-  // A chunk with many survivors (the running bounds are still low) is
-  // deferred: recorded with its largest key and read again at the end, and
-  // only if that key reaches the final bound.
-  if (may_defer && cnt > (uint32_t)DCHUNK) {
+  for (int q = 0; q < NGRP; ++q) {
+    float g = __uint_as_float(kb[q * GRP]);
+#pragma unroll
+    for (int j = 1; j < GRP; ++j) g = fmaxf(g, __uint_as_float(kb[q * GRP + j]));
+    gmax[q] = g;
+    lmax = fmaxf(lmax, g);
+  }
+  bool keep_any = true;
+  if (may_defer && __popcll(__ballot(lmax >= thf)) > DLANES) {
     uint32_t idx = 0;
     if (lane == 0) idx = atomicAdd(&sh.ndef, 1u);
     idx = (uint32_t)__builtin_amdgcn_readfirstlane((int)idx);
     if (idx < (uint32_t)DEFCAP) {
       if (lane == 0) fl.def[idx] = make_uint2((uint32_t)c, cmax);
-      cnt = 0;
+      keep_any = false;
+      tany = lo;
+      if (!(key2f(cmax) >= tany)) return;
     }
   }
-  uint32_t base = 0;
-  if (cnt) {
-    if (lane == 0) base = atomicAdd(&sh.count, cnt);
-    base = (uint32_t)__builtin_amdgcn_readfirstlane((int)base);
-  }
-  const bool spill_now = base + cnt > (uint32_t)BUFCAP;
-  const bool skip = cnt == 0u;
-  const float tany = (spill_now || skip) ? lo : fminf(thf, lo);
-  uint32_t off = base;
+  const uint32_t eb = (uint32_t)c * WSEG + (uint32_t)lane * GRP;
+  bool spilled = false;
 #pragma unroll
-  for (int i = 0; i < EPT; ++i) {
-    const float v = __uint_as_float(kb[i]);
-    if (__ballot(v >= tany)) {
+  for (int q = 0; q < NGRP; ++q) {
+    if (!__ballot(gmax[q] >= tany)) continue;
+#pragma unroll
+    for (int j = 0; j < GRP; ++j) {
+      const int i = q * GRP + j;
+      const float v = __uint_as_float(kb[i]);
+      if (!__ballot(v >= tany)) continue;
       if (v >= lo) ws.acc += (double)__builtin_amdgcn_exp2f((v - ws.m_ref) * 1.4426950408889634f);
-      if (!spill_now && !skip) {
+      if (keep_any) {
         const bool k = v >= thf;
         const uint64_t km = __ballot(k);
-        if (k)
-          fl.buf[off + lanes_below(km)] =
-              pack(f2key(__float_as_uint(v)), eb + (uint32_t)((i / GRP) * 64 * GRP + (i % GRP)));
-        off += (uint32_t)__popcll(km);
+        if (km) {
+          const int first = (int)__builtin_ctzll(km);
+          uint32_t base = 0;
+          if (lane == first) base = atomicAdd(&sh.count, (uint32_t)__popcll(km));
+          base = (uint32_t)__builtin_amdgcn_readlane((int)base, first);
+          const uint32_t slot = base + lanes_below(km);
+          const uint64_t e = pack(f2key(__float_as_uint(v)), eb + (uint32_t)(q * 64 * GRP + j));
+          if (base + (uint32_t)__popcll(km) <= (uint32_t)BUFCAP) {
+            if (k) fl.buf[slot] = e;
+          } else {
+            // rare: the buffer is full; below BUFCAP to LDS, the rest to
+            // the spill area (never one store to either space)
+            if (k && slot < (uint32_t)BUFCAP) fl.buf[slot] = e;
+            if (k && slot >= (uint32_t)BUFCAP) __builtin_nontemporal_store(e, &spill[slot - BUFCAP]);
+            spilled = true;
+          }
+        }
       }
     }
   }
-  if (spill_now) {
-    // rare: the buffer is full. Slots below BUFCAP to LDS, the rest to the
-    // spill area, in separate loops (never one store to either space)
-    off = base;
-#pragma unroll
-    for (int i = 0; i < EPT; ++i) {
-      const float v = __uint_as_float(kb[i]);
-      const bool k = v >= thf;
-      const uint64_t km = __ballot(k);
-      const uint32_t slot = off + lanes_below(km);
-      if (k && slot < (uint32_t)BUFCAP)
-        fl.buf[slot] = pack(f2key(__float_as_uint(v)), eb + (uint32_t)((i / GRP) * 64 * GRP + (i % GRP)));
-      off += (uint32_t)__popcll(km);
-    }
-    off = base;
-#pragma unroll
-    for (int i = 0; i < EPT; ++i) {
-      const float v = __uint_as_float(kb[i]);
-      const bool k = v >= thf;
-      const uint64_t km = __ballot(k);
-      const uint32_t slot = off + lanes_below(km);
-      if (k && slot >= (uint32_t)BUFCAP)
-        __builtin_nontemporal_store(
-            pack(f2key(__float_as_uint(v)), eb + (uint32_t)((i / GRP) * 64 * GRP + (i % GRP))),
-            &spill[slot - BUFCAP]);
-      off += (uint32_t)__popcll(km);
-    }
-    __builtin_amdgcn_s_waitcnt(0);
-  }
+  if (spilled) __builtin_amdgcn_s_waitcnt(0);
 }
 
 // Order-free parallel compaction: appends to dst the entries of src[0, n)
@@ -1121,23 +1204,21 @@ __global__ __launch_bounds__(NT) void smp_row(SmpArgs A) {
     step(buf0, c, c == wave);
     if (c + NW < nch) step(buf1, c + NW, false);
   }
-  // the exact bound of the union of the waves' lists (8 * KB distinct
-  // elements): the KB-th largest of them
-  if (lane < plan.KB) fl.lists[wave * plan.KB + lane] = lst;
+  // A final bound from the union of the waves' lists: the KB-th largest of
+  // their top 8 entries (64 distinct elements, ranked by one wave). It is at
+  // least the minimum over the waves of their ceil(KB/8)-th values, and
+  // sh.theta keeps the best single-wave bound: no bound used in the stream
+  // exceeds the final one, which keeps the buffer complete down to it.
+  if (lane < 8) fl.lists[wave * 8 + lane] = lane < plan.KB ? lst : 0u;
   __syncthreads();  // every append, deferral, list and maximum is in LDS
-  {
-    const int nl = NW * plan.KB;
-    for (int t = tid; t < nl; t += NT) {
-      const uint32_t x = fl.lists[t];
-      if (x != 0u) {
-        int rank = 0;
-        for (int j = 0; j < nl; ++j) {
-          const uint32_t y = fl.lists[j];
-          rank += (y > x || (y == x && j < t)) ? 1 : 0;
-        }
-        if (rank == plan.KB - 1) atomicMax(&sh.theta, x);
-      }
+  if (wave == 0) {
+    const uint32_t x = fl.lists[lane];
+    uint32_t rank = 0;
+    for (int j = 0; j < 64; ++j) {
+      const uint32_t y = (uint32_t)__builtin_amdgcn_readlane((int)x, j);
+      rank += (y > x || (y == x && j < lane)) ? 1u : 0u;
     }
+    if (x != 0u && rank == (uint32_t)(plan.KB - 1)) atomicMax(&sh.theta, x);
   }
   __syncthreads();
   const uint32_t theta = sh.theta;
@@ -1175,11 +1256,10 @@ __global__ __launch_bounds__(NT) void smp_row(SmpArgs A) {
   const uint32_t rflags = sh.flags;
   double logZ = 0.0;
   if (A.want_mass) {
-    double part = 0.0;
-#pragma unroll
-    for (int w = 0; w < NW; ++w)
-      if (s_mref[w] != -__builtin_inff()) part += s_mass[w] * exp((double)s_mref[w] - (double)M);
-    logZ = log(part);
+    // one term per wave, in lanes 0..NW-1 of every wave
+    double t = 0.0;
+    if (lane < NW && s_mref[lane] != -__builtin_inff()) t = s_mass[lane] * exp((double)s_mref[lane] - (double)M);
+    logZ = log(wave_sum_f64(t));
   }
   int32_t status = ST_OK;
   if (rflags & F_INVALID) status = ST_EINVAL;
@@ -1193,20 +1273,52 @@ __global__ __launch_bounds__(NT) void smp_row(SmpArgs A) {
     const uint32_t theta_f = row_threshold(plan, P, M, theta);
     bool dense = A.force_dense != 0;
     int64_t ncand = 0;
+    bool sorted = false;
     if (!dense) {
       const uint32_t cnt = sh.count;
-      const uint32_t n = cnt < (uint32_t)BUFCAP ? cnt : (uint32_t)BUFCAP;
-      uint32_t nc = compact_entries(fl.buf, n, fl.cand, CAP, theta_f, &sh.ctr, true);
-      if (cnt > (uint32_t)BUFCAP)
+      if (cnt <= (uint32_t)BUFCAP) {
+        // wave 0 alone: order-free compaction of the buffer, then (<= 64
+        // survivors, the common case) a rank sort by broadcast comparisons
+        if (wave == 0) {
+          uint32_t m = 0;
+          for (uint32_t i0 = 0; i0 < cnt; i0 += 64) {
+            const uint32_t i = i0 + (uint32_t)lane;
+            const uint64_t e = i < cnt ? fl.buf[i] : 0ull;
+            const bool k = i < cnt && pk_key(e) >= theta_f;
+            const uint64_t km = __ballot(k);
+            const uint32_t slot = m + lanes_below(km);
+            if (k && slot < (uint32_t)CAP) fl.cand[slot] = e;
+            m += (uint32_t)__popcll(km);
+          }
+          if (m <= 64u) {
+            const uint64_t x = (uint32_t)lane < m ? fl.cand[lane] : 0ull;
+            uint32_t rank = 0;
+            for (uint32_t j = 0; j < m; ++j) {
+              const uint64_t y = ((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(x >> 32), (int)j) << 32) |
+                                 (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)x, (int)j);
+              rank += y > x ? 1u : 0u;
+            }
+            if ((uint32_t)lane < m) fl.cand[rank] = x;
+          }
+          if (lane == 0) sh.ctr = m;
+        }
+        __syncthreads();
+        ncand = (int64_t)sh.ctr;
+        sorted = ncand <= 64;
+      } else {
+        uint32_t nc = compact_entries(fl.buf, BUFCAP, fl.cand, CAP, theta_f, &sh.ctr, true);
         nc = compact_entries(spill, cnt - (uint32_t)BUFCAP, fl.cand, CAP, theta_f, &sh.ctr, false);
-      ncand = (int64_t)nc;
+        ncand = (int64_t)nc;
+      }
       dense = ncand > CAP || ncand < 1;
     }
     const uint64_t* cand;
     double* wbuf;
     if (!dense) {
-      if (ncand <= NT) sort_desc_small(fl.cand, (uint64_t*)fl.w, (int)ncand);
-      else sort_desc(fl.cand, (int)ncand);
+      if (!sorted) {
+        if (ncand <= NT) sort_desc_small(fl.cand, (uint64_t*)fl.w, (int)ncand);
+        else sort_desc(fl.cand, (int)ncand);
+      }
       cand = fl.cand;
       wbuf = fl.w;
     } else {
@@ -1223,61 +1335,76 @@ __global__ __launch_bounds__(NT) void smp_row(SmpArgs A) {
     // value, then smaller id).
     const uint32_t amax = pk_id(cand[0]);
 
-    // ---- outputs in raw order ------------------------------------------
-    if (A.argmax && tid == 0) A.argmax[row] = amax;
-    if (A.top8_ids) {
-      for (int i = tid; i < 8; i += NT) {
-        const bool in = i < ncand;
-        const uint32_t id = in ? pk_id(cand[i]) : 0xffffffffu;
-        A.top8_ids[(int64_t)row * 8 + i] = id;
-        A.top8_vals[(int64_t)row * 8 + i] = in ? __uint_as_float(value_bits<DT, PEN>(rc, id)) : -__builtin_inff();
-      }
+    // ---- outputs in raw order (wave 1, while wave 0 draws) ----------------
+    // Raw values come from the keys (exact for every value but +-0, whose
+    // sign the key drops, and for penalised rows, whose keys are of the
+    // penalised values): only those are read again from the logits.
+    const int ot = tid - 64;  // wave 1's lanes: 0..63
+    auto raw_value = [&](uint64_t p) -> float {
+      const float v = key2f(pk_key(p));
+      if (PEN || v == 0.0f) return __uint_as_float(value_bits<DT, PEN>(rc, pk_id(p)));
+      return v;
+    };
+    if (A.argmax && ot == 0) A.argmax[row] = amax;
+    if (A.top8_ids && ot >= 0 && ot < 8) {
+      const int i = ot;
+      const bool in = i < ncand;
+      A.top8_ids[(int64_t)row * 8 + i] = in ? pk_id(cand[i]) : 0xffffffffu;
+      A.top8_vals[(int64_t)row * 8 + i] = in ? raw_value(cand[i]) : -__builtin_inff();
     }
-    if (A.top20_ids) {
-      for (int i = tid; i < 20; i += NT) {
-        const bool in = i < ncand;
-        const uint32_t id = in ? pk_id(cand[i]) : 0xffffffffu;
-        A.top20_ids[(int64_t)row * 20 + i] = id;
-        A.top20_vals[(int64_t)row * 20 + i] = in ? __uint_as_float(value_bits<DT, PEN>(rc, id)) : -__builtin_inff();
-      }
+    if (A.top20_ids && ot >= 0 && ot < 20) {
+      const int i = ot;
+      const bool in = i < ncand;
+      A.top20_ids[(int64_t)row * 20 + i] = in ? pk_id(cand[i]) : 0xffffffffu;
+      A.top20_vals[(int64_t)row * 20 + i] = in ? raw_value(cand[i]) : -__builtin_inff();
     }
-    if (A.topn_ids) {
-      for (int i = tid; i < A.topn; i += NT) {
-        const bool in = i < ncand;
-        const uint32_t id = in ? pk_id(cand[i]) : 0xffffffffu;
-        A.topn_ids[(int64_t)row * A.topn + i] = id;
-        if (A.topn_vals)
-          A.topn_vals[(int64_t)row * A.topn + i] = in ? __uint_as_float(value_bits<DT, PEN>(rc, id)) : -__builtin_inff();
-      }
+    if (A.topn_ids && ot >= 0 && ot < A.topn) {
+      const int i = ot;
+      const bool in = i < ncand;
+      A.topn_ids[(int64_t)row * A.topn + i] = in ? pk_id(cand[i]) : 0xffffffffu;
+      if (A.topn_vals) A.topn_vals[(int64_t)row * A.topn + i] = in ? raw_value(cand[i]) : -__builtin_inff();
     }
-    if (A.n_lp > 0) {
-      for (int i = tid; i < A.n_lp; i += NT) {
-        const bool in = i < ncand;
-        const uint32_t id = in ? pk_id(cand[i]) : 0xffffffffu;
-        double lp = -__builtin_inf();
-        if (in) {
-          const float l = __uint_as_float(value_bits<DT, PEN>(rc, id));
-          lp = ((double)l - (double)M) - logZ;
-        }
-        A.lp_ids[(int64_t)row * A.n_lp + i] = id;
-        A.lp_vals[(int64_t)row * A.n_lp + i] = lp;
+    if (A.n_lp > 0 && ot >= 0 && ot < A.n_lp) {
+      const int i = ot;
+      const bool in = i < ncand;
+      double lp = -__builtin_inf();
+      if (in) {
+        // (the sign of a zero does not change l - M)
+        const float l = PEN ? __uint_as_float(value_bits<DT, PEN>(rc, pk_id(cand[i]))) : key2f(pk_key(cand[i]));
+        lp = ((double)l - (double)M) - logZ;
       }
+      A.lp_ids[(int64_t)row * A.n_lp + i] = in ? pk_id(cand[i]) : 0xffffffffu;
+      A.lp_vals[(int64_t)row * A.n_lp + i] = lp;
     }
-    if (A.nll_targets && tid == 0) {
+    if (A.nll_targets && ot == 0) {
       const uint32_t t = A.nll_targets[row];
       if (t < (uint32_t)V) {
         const float l = __uint_as_float(value_bits<DT, PEN>(rc, t));
         A.nll_out[row] = ((double)M - (double)l) + logZ;
       } else {
-        status = ST_EINVAL;
         A.nll_out[row] = __builtin_nan("");
       }
+    }
+    if (A.nll_targets) {
+      // an out-of-range target fails the row (every thread sees the same)
+      if (A.nll_targets[row] >= (uint32_t)V) status = ST_EINVAL;
     }
     // ---- token selection ---------------------------------------------------
     if (A.out_ids) {
       if (P.greedy) {
         const int nd = A.mode == MODE_VERIFY ? 1 : A.n_draws;
         for (int d = tid; d < nd; d += NT) A.out_ids[(int64_t)row * A.n_draws + d] = amax;
+      } else if (ncand <= 64 && (A.mode == MODE_VERIFY || A.n_draws == 1)) {
+        // one draw over at most 64 candidates: wave 0 alone
+        if (wave == 0) {
+          int c = (int)plan.k_eff < (int)ncand ? (int)plan.k_eff : (int)ncand;
+          if (plan.need_rel) {
+            const uint32_t trel = relevance_key(M, P.temperature);
+            const int nrel = (int)__popcll(__ballot(lane < ncand && pk_key(cand[lane < ncand ? lane : 0]) >= trel));
+            c = (int)plan.k_eff < nrel ? (int)plan.k_eff : nrel;
+          }
+          sample_tail_wave(A, P, row, cand, c);
+        }
       } else {
         int64_t c;
         if (plan.need_rel) {
