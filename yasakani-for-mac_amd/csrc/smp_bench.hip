@@ -211,10 +211,9 @@ int main(int argc, char** argv) {
   if (yskn_smp_get_stats(h, s, 4) < 0) check(-1, "yskn_smp_get_stats");  // returns the count
   printf("{\"mode\": \"sample\", \"rows\": %d, \"vocab\": %d, \"steps\": %d, \"warmup\": %d, "
          "\"us_per_step\": %.3f, \"rows_per_s\": %.1f, \"hbm_gbs\": %.1f, \"ids_digest\": \"%016llx\", "
-         "\"dense_rows\": %llu, \"rescan_waves\": %llu, \"candidates\": %llu}\n",
+         "\"dense_rows\": %llu, \"candidates\": %llu}\n",
          rows, V, steps, warmup, us, rows / us * 1e6, (double)bytes / us / 1e3,
-         (unsigned long long)digest, (unsigned long long)s[1], (unsigned long long)s[2],
-         (unsigned long long)s[3]);
+         (unsigned long long)digest, (unsigned long long)s[1], (unsigned long long)s[3]);
   for (auto& e : ev) HIP_OK(hipEventDestroy(e));
   yskn_smp_destroy(h);
   for (auto& b : buf) HIP_OK(hipFree(b));

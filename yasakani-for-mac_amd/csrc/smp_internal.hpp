@@ -57,7 +57,7 @@ enum StatIndex {
   STAT_ROWS = 0,      // rows finished
   STAT_DENSE_ROWS,    // rows served by the exact large-candidate path
   STAT_RESCAN_WAVES,  // always 0 (kept for the counter layout of the C ABI)
-  STAT_CANDIDATES,    // survivors sorted by finishers
+  STAT_CANDIDATES,    // candidates sorted by the row blocks
   STAT_COUNT
 };
 

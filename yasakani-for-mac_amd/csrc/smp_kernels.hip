@@ -824,7 +824,7 @@ __device__ void sort_desc_small(uint64_t* a, uint64_t* b, int n) {
 }
 
 // ---------------------------------------------------------------------------
-// smp_finish: one block per row.
+// LDS of a row block (136 KB in all with the small arrays: one block per CU).
 // ---------------------------------------------------------------------------
 struct RowLds {
   uint64_t buf[BUFCAP];    // append buffer of candidates (unordered)
@@ -964,12 +964,12 @@ __device__ __forceinline__ void chunk_max(float lmax, WaveState& ws, RowShared& 
 // global memory (each element is appended at most once, so V entries always
 // suffice); that rare path ends with a full wait, so the common path holds
 // only LDS stores and the compiler can keep the prefetched chunk in flight.
-// A chunk where many lanes hold survivors (the running bounds are still low)
-// is deferred instead: recorded with its largest key and read again at the
+// A chunk where more than defer_lanes lanes hold survivors (the running
+// bounds are still low; 64: never) is deferred instead: recorded with its largest key and read again at the
 // end, and only if that key reaches the final bound.
 template <int DT>
 __device__ __forceinline__ void chunk_filter(int c, int lane, const uint32_t (&kb)[EPT], uint32_t thr,
-                                             uint32_t mk, bool mass, uint32_t cmax, bool may_defer,
+                                             uint32_t mk, bool mass, uint32_t cmax, int defer_lanes,
                                              WaveState& ws, RowShared& sh, RowLds& fl, uint64_t* spill) {
   constexpr int GRP = (DT == 0) ? 4 : 8;
   constexpr int NGRP = EPT / GRP;
@@ -998,7 +998,7 @@ __device__ __forceinline__ void chunk_filter(int c, int lane, const uint32_t (&k
     lmax = fmaxf(lmax, g);
   }
   bool keep_any = true;
-  if (may_defer && __popcll(__ballot(lmax >= thf)) > DLANES) {
+  if (defer_lanes < 64 && __popcll(__ballot(lmax >= thf)) > defer_lanes) {
     uint32_t idx = 0;
     if (lane == 0) idx = atomicAdd(&sh.ndef, 1u);
     idx = (uint32_t)__builtin_amdgcn_readfirstlane((int)idx);
@@ -1197,7 +1197,11 @@ __global__ __launch_bounds__(NT) void smp_row(SmpArgs A) {
         __hip_atomic_load(&sh.mkey, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP));
     mk = mk > ws.wkey ? mk : ws.wkey;
     const uint32_t thr = A.force_dense ? 0xffffffffu : row_threshold(plan, P, key2f(mk), th);
-    chunk_filter<DT>(c, lane, X, thr, mk, A.want_mass != 0, cmax, true, ws, sh, fl, spill);
+    // (a wave's first chunk has about KB lanes with survivors by
+    // construction -- the lane maxima that set its first bound -- so its
+    // deferral limit is raised by KB)
+    chunk_filter<DT>(c, lane, X, thr, mk, A.want_mass != 0, cmax, first ? DLANES + plan.KB : DLANES, ws, sh,
+                     fl, spill);
     load_chunk<DT, VEC>(rc, V, nch, c + 2 * NW, lane, X);
   };
   for (int c = wave; c < nch; c += 2 * NW) {
@@ -1223,21 +1227,38 @@ __global__ __launch_bounds__(NT) void smp_row(SmpArgs A) {
   __syncthreads();
   const uint32_t theta = sh.theta;
   // deferred chunks whose largest key reaches the final bound: read again
-  // and filter with that bound (the wave with the entry's index mod NW)
+  // and filter with that bound. Entry i belongs to wave i % NW; each wave
+  // keeps two of its chunks in flight (the stream's buffers are free now).
   if (!A.force_dense) {
     const uint32_t mkf = sh.mkey;
     const uint32_t thr_f = row_threshold(plan, P, key2f(mkf), theta);
     const uint32_t nd = sh.ndef < (uint32_t)DEFCAP ? sh.ndef : (uint32_t)DEFCAP;
-    for (uint32_t i = (uint32_t)wave; i < nd; i += NW) {
-      const uint2 d = fl.def[i];
-      if (d.y >= thr_f) {
-        uint32_t kb[EPT];
-        load_chunk<DT, VEC>(rc, V, nch, (int)d.x, lane, kb);
-        float lmax = -__builtin_inff();
-        bool bad = false;
-        chunk_values<DT, PEN>(rc, V, (int)d.x, lane, kb, lmax, bad);
-        chunk_filter<DT>((int)d.x, lane, kb, thr_f, mkf, false, d.y, false, ws, sh, fl, spill);
-      }
+    auto next = [&](uint32_t from) -> uint32_t {
+      for (uint32_t i = from; i < nd; i += NW)
+        if (fl.def[i].y >= thr_f) return i;
+      return nd;
+    };
+    auto redo = [&](uint32_t (&X)[EPT], uint32_t i) {
+      const int cc = (int)fl.def[i].x;
+      float lmax = -__builtin_inff();
+      bool bad = false;
+      chunk_values<DT, PEN>(rc, V, cc, lane, X, lmax, bad);
+      chunk_filter<DT>(cc, lane, X, thr_f, mkf, false, fl.def[i].y, 64, ws, sh, fl, spill);
+    };
+    uint32_t ia = next((uint32_t)wave);
+    uint32_t ib = ia < nd ? next(ia + NW) : nd;
+    if (ia < nd) load_chunk<DT, VEC>(rc, V, nch, (int)fl.def[ia].x, lane, buf0);
+    if (ib < nd) load_chunk<DT, VEC>(rc, V, nch, (int)fl.def[ib].x, lane, buf1);
+    while (ia < nd) {
+      redo(buf0, ia);
+      const uint32_t ic = ib < nd ? next(ib + NW) : nd;
+      if (ic < nd) load_chunk<DT, VEC>(rc, V, nch, (int)fl.def[ic].x, lane, buf0);
+      if (ib >= nd) break;
+      redo(buf1, ib);
+      const uint32_t id = ic < nd ? next(ic + NW) : nd;
+      if (id < nd) load_chunk<DT, VEC>(rc, V, nch, (int)fl.def[id].x, lane, buf1);
+      ia = ic;
+      ib = id;
     }
   }
   if (__ballot(ws.bad)) wflags |= F_NONFINITE;

@@ -392,7 +392,7 @@ class DeviceSampler:
     def sync(self) -> None:
         _raise(self.L.yskn_smp_sync(self.h, self._stream()))
 
-    STAT_NAMES = ("rows", "dense_rows", "rescan_waves", "candidates")
+    STAT_NAMES = ("rows", "dense_rows", "reserved", "candidates")
 
     def stats(self) -> dict:
         """Cumulative profiling counters of the handle (synchronises)."""
