@@ -210,7 +210,7 @@ int yskn_smp_sync(yskn_smp_handle h, void* stream);
 
 /* Host-slice convenience with the exact signature semantics of the Rust
  * trait Selector::select(&mut self, logits: &[f32], prediction_position: u64)
- * (crates/yskn-ref/src/speculation.rs:121-131): copies `vocab` host logits to
+ * (crates/yskn-ref/src/speculation.rs:123-139): copies `vocab` host logits to
  * the device, samples with row-0 parameters, returns the token synchronously. */
 int yskn_smp_select_host(yskn_smp_handle h, const float* host_logits, int32_t vocab,
                          uint64_t prediction_position, uint32_t* out_token);

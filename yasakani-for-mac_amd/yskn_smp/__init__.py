@@ -9,7 +9,7 @@ read like the reference's own:
   prediction_position)`` -- output_head_sampler.rs:77-92
 * ``greedy``, ``top_tokens``, ``negative_log_likelihood`` --
   output_head_sampler.rs:103-134,230-250
-* ``select`` (the ``Selector`` trait, crates/yskn-ref/src/speculation.rs:121-131)
+* ``select`` (the ``Selector`` trait, crates/yskn-ref/src/speculation.rs:123-139)
 * ``verify`` -- the acceptance loop of speculation.rs:483-523
 
 Errors are raised as ``InvalidInput`` / ``NonFinite`` (lib.rs:37-45).
@@ -403,7 +403,7 @@ class DeviceSampler:
         return {k: int(buf[i]) for i, k in enumerate(self.STAT_NAMES[:n])}
 
     def select(self, logits: np.ndarray, prediction_position: int) -> int:
-        """Selector::select on a host slice (speculation.rs:121-131)."""
+        """Selector::select on a host slice (speculation.rs:123-139)."""
         a = np.ascontiguousarray(logits, dtype=np.float32)
         out = C.c_uint32()
         _raise(self.L.yskn_smp_select_host(self.h, a.ctypes.data, a.size, prediction_position,
