@@ -33,6 +33,13 @@ namespace yskn {
 
 constexpr int32_t YSKN_V3 = 3;
 
+// Pointers typed with their address space (3: LDS, 1: global). Stores through
+// them cannot be merged into one generic (flat) store when the two kinds sit
+// in neighbouring branches; a flat access counts against both the vector
+// memory and the LDS counters, so every wait after it becomes a full wait.
+typedef __attribute__((address_space(3))) uint64_t lds_u64;
+typedef __attribute__((address_space(1))) uint64_t global_u64;
+
 // ---------------------------------------------------------------------------
 // keys and packing
 // ---------------------------------------------------------------------------
@@ -880,6 +887,45 @@ __device__ __forceinline__ void load_chunk(const RowCtx& rc, int32_t V, int nch,
   }
 }
 
+// Raw bits of full chunk c through 16-byte buffer loads, no guards: the
+// caller ensures the chunk lies inside the row and the row is 16-byte
+// aligned. The loads take a uniform chunk offset in an SGPR and
+// loop-invariant lane offsets in VGPRs, so the stream spends no vector
+// instructions on addresses. With `live` false the same loads go through a
+// resource of size 0: every one is out of range, returns zeros and touches
+// no memory. Issuing the same loads on every path, and keeping address
+// arithmetic out of the destination registers, lets the compiler wait for
+// exactly the buffer it is about to read, with the other still in flight.
+template <int DT>
+__device__ __forceinline__ void load_full(const char* row_base, int32_t V, int c, bool live, int lane,
+                                          uint32_t (&kb)[EPT]) {
+  constexpr int GRP = (DT == 0) ? 4 : 8;
+  constexpr int NGRP = EPT / GRP;
+  const __amdgpu_buffer_rsrc_t rs =
+      __builtin_amdgcn_make_buffer_rsrc((void*)row_base, (short)0, live ? V * (DT == 0 ? 4 : 2) : 0, 0x00020000);
+  const int soff = live ? c * WSEG * (DT == 0 ? 4 : 2) : 0;
+#pragma unroll
+  for (int q = 0; q < NGRP; ++q) {
+    const __attribute__((ext_vector_type(4))) uint32_t v =
+        __builtin_amdgcn_raw_buffer_load_b128(rs, lane * 16 + (q & 3) * 1024, soff + (q >> 2) * 4096, 0);
+    if (DT == 0) {
+      kb[q * 4 + 0] = v.x;
+      kb[q * 4 + 1] = v.y;
+      kb[q * 4 + 2] = v.z;
+      kb[q * 4 + 3] = v.w;
+    } else {
+      kb[q * 8 + 0] = v.x << 16;
+      kb[q * 8 + 1] = v.x & 0xffff0000u;
+      kb[q * 8 + 2] = v.y << 16;
+      kb[q * 8 + 3] = v.y & 0xffff0000u;
+      kb[q * 8 + 4] = v.z << 16;
+      kb[q * 8 + 5] = v.z & 0xffff0000u;
+      kb[q * 8 + 6] = v.w << 16;
+      kb[q * 8 + 7] = v.w & 0xffff0000u;
+    }
+  }
+}
+
 // Chunk c's raw bits -> binary32 value bits in place (penalties applied,
 // absent elements -inf); non-finite test and lane maximum.
 template <int DT, bool PEN>
@@ -1031,12 +1077,12 @@ __device__ __forceinline__ void chunk_filter(int c, int lane, const uint32_t (&k
           const uint32_t slot = base + lanes_below(km);
           const uint64_t e = pack(f2key(__float_as_uint(v)), eb + (uint32_t)(q * 64 * GRP + j));
           if (base + (uint32_t)__popcll(km) <= (uint32_t)BUFCAP) {
-            if (k) fl.buf[slot] = e;
+            if (k) ((lds_u64*)fl.buf)[slot] = e;
           } else {
             // rare: the buffer is full; below BUFCAP to LDS, the rest to
-            // the spill area (never one store to either space)
-            if (k && slot < (uint32_t)BUFCAP) fl.buf[slot] = e;
-            if (k && slot >= (uint32_t)BUFCAP) __builtin_nontemporal_store(e, &spill[slot - BUFCAP]);
+            // the spill area
+            if (k && slot < (uint32_t)BUFCAP) ((lds_u64*)fl.buf)[slot] = e;
+            if (k && slot >= (uint32_t)BUFCAP) __builtin_nontemporal_store(e, &((global_u64*)spill)[slot - BUFCAP]);
             spilled = true;
           }
         }
@@ -1129,9 +1175,14 @@ __global__ __launch_bounds__(NT) void smp_row(SmpArgs A) {
   ws.m_ref = -__builtin_inff();
   ws.acc = 0.0;
   ws.bad = false;
+  // Chunks [0, nfull) are read by the double-buffered stream with unguarded
+  // 16-byte loads; the rest (the ragged last chunk of an aligned row, every
+  // chunk of an unaligned one) through the guarded path after it.
+  const int nfull = VEC ? V / WSEG : 0;
   uint32_t buf0[EPT], buf1[EPT];
-  load_chunk<DT, VEC>(rc, V, nch, wave, lane, buf0);
-  load_chunk<DT, VEC>(rc, V, nch, wave + NW, lane, buf1);
+  load_full<DT>(rc.base, V, wave, wave < nfull, lane, buf0);
+  __builtin_amdgcn_sched_barrier(0);  // buf0's loads first: the stream waits for them first
+  load_full<DT>(rc.base, V, wave + NW, wave + NW < nfull, lane, buf1);
   __builtin_amdgcn_sched_barrier(0);  // both chunks in flight before any work
   __syncthreads();  // shared state initialised
 
@@ -1147,8 +1198,9 @@ __global__ __launch_bounds__(NT) void smp_row(SmpArgs A) {
   const int r_first = plan.KB < 64 ? plan.KB : 64;
   const int r_next = plan.KB < 8 ? plan.KB : 8;
 
-  // one chunk: c from X; prefetch the wave's chunk two steps ahead into X
-  auto step = [&](uint32_t (&X)[EPT], int c, bool first) {
+  // one chunk: c from X; in the stream, prefetch the wave's chunk two steps
+  // ahead into X
+  auto step = [&](uint32_t (&X)[EPT], int c, bool first, bool stream) {
     float lmax = -__builtin_inff();
     chunk_values<DT, PEN>(rc, V, c, lane, X, lmax, ws.bad);
     uint32_t lk = lmax == -__builtin_inff() ? 0u : f2key(__float_as_uint(lmax));
@@ -1202,11 +1254,21 @@ __global__ __launch_bounds__(NT) void smp_row(SmpArgs A) {
     // deferral limit is raised by KB)
     chunk_filter<DT>(c, lane, X, thr, mk, A.want_mass != 0, cmax, first ? DLANES + plan.KB : DLANES, ws, sh,
                      fl, spill);
-    load_chunk<DT, VEC>(rc, V, nch, c + 2 * NW, lane, X);
+    if (stream) load_full<DT>(rc.base, V, c + 2 * NW, c + 2 * NW < nfull, lane, X);
   };
-  for (int c = wave; c < nch; c += 2 * NW) {
-    step(buf0, c, c == wave);
-    if (c + NW < nch) step(buf1, c + NW, false);
+  // pairs of steps with no condition between them: at every step the buffer
+  // read is the older of the two in flight, on entry and around the loop
+  const int nmine = wave < nfull ? (nfull - wave + NW - 1) / NW : 0;
+  int c = wave;
+  for (int i = 0; i + 1 < nmine; i += 2, c += 2 * NW) {
+    step(buf0, c, i == 0, true);
+    step(buf1, c + NW, false, true);
+  }
+  if (nmine & 1) step(buf0, c, nmine == 1, true);
+  // the remaining chunks, each by the wave the round-robin order gives it
+  for (c = nfull + (wave - nfull % NW + NW) % NW; c < nch; c += NW) {
+    load_chunk<DT, VEC>(rc, V, nch, c, lane, buf0);
+    step(buf0, c, c == wave, false);
   }
   // A final bound from the union of the waves' lists: the KB-th largest of
   // their top 8 entries (64 distinct elements, ranked by one wave). It is at
