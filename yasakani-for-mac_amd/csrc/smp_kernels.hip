@@ -135,6 +135,61 @@ __device__ __forceinline__ double wave_sum_f64(double v) {
   for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
   return v;
 }
+// A 64-bit value moved by one DPP pattern (both halves; lanes the pattern
+// does not write read 0).
+template <int CTRL, int ROWS>
+__device__ __forceinline__ uint64_t dpp_u64(uint64_t v) {
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)v, CTRL, ROWS, 0xf, false);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)(v >> 32), CTRL, ROWS, 0xf, false);
+  return ((uint64_t)hi << 32) | lo;
+}
+__device__ __forceinline__ uint64_t lane_u64(uint64_t v, int j) {
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)v, j);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(v >> 32), j);
+  return ((uint64_t)hi << 32) | lo;
+}
+// Wave-wide binary64 sum through DPP (scan within rows of 16, then row
+// broadcasts; no LDS round trips), returned to every lane. The adds are not
+// in serial order: for the logprob mass only, never for a top-p total.
+__device__ __forceinline__ double wave_sum_f64_dpp(double v) {
+  auto add = [](double a, uint64_t b) { return a + __longlong_as_double((long long)b); };
+  v = add(v, dpp_u64<0x111, 0xf>((uint64_t)__double_as_longlong(v)));  // row_shr:1
+  v = add(v, dpp_u64<0x112, 0xf>((uint64_t)__double_as_longlong(v)));  // row_shr:2
+  v = add(v, dpp_u64<0x114, 0xf>((uint64_t)__double_as_longlong(v)));  // row_shr:4
+  v = add(v, dpp_u64<0x118, 0xf>((uint64_t)__double_as_longlong(v)));  // row_shr:8
+  v = add(v, dpp_u64<0x142, 0xa>((uint64_t)__double_as_longlong(v)));  // row_bcast:15
+  v = add(v, dpp_u64<0x143, 0xc>((uint64_t)__double_as_longlong(v)));  // row_bcast:31
+  return __longlong_as_double((long long)lane_u64((uint64_t)__double_as_longlong(v), 63));
+}
+// Wave-wide maximum of 64-bit values through DPP, returned to every lane.
+__device__ __forceinline__ uint64_t wave_max_u64_dpp(uint64_t v) {
+  uint64_t t;
+  t = dpp_u64<0x111, 0xf>(v);
+  v = v > t ? v : t;
+  t = dpp_u64<0x112, 0xf>(v);
+  v = v > t ? v : t;
+  t = dpp_u64<0x114, 0xf>(v);
+  v = v > t ? v : t;
+  t = dpp_u64<0x118, 0xf>(v);
+  v = v > t ? v : t;
+  t = dpp_u64<0x142, 0xa>(v);
+  v = v > t ? v : t;
+  t = dpp_u64<0x143, 0xc>(v);
+  v = v > t ? v : t;
+  return lane_u64(v, 63);
+}
+// The largest t with at least k (1 <= k <= 64) lanes holding a value >= t:
+// the k-th largest of the 64 values (0 if fewer than k are nonzero), found
+// bit by bit from the top with one ballot per bit.
+__device__ __forceinline__ uint32_t wave_kth_largest_radix(uint32_t x, int k) {
+  uint32_t t = 0u;
+#pragma unroll
+  for (int b = 31; b >= 0; --b) {
+    const uint32_t u = t | (1u << b);
+    if (__popcll(__ballot(x >= u)) >= (uint32_t)k) t = u;
+  }
+  return t;
+}
 __device__ __forceinline__ int wave_sum_int(int v) {
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
@@ -487,52 +542,41 @@ __device__ __forceinline__ void sample_tail_wave(const SmpArgs& A, const DevPara
     w = exp_d(z);
     if (P.version == YSKN_V3) sc = z + gumbel_from_key(position_key(P.seed, pos), pk_id(cj));
   }
-  // top-p: first n with prefix >= top_p * total (serial sums in candidate order)
-  double total = 0.0;
-  for (int j = 0; j < c; ++j) total = total + lane_f64(w, j);
-  const double thr = P.top_p * total;
-  int n = c;
-  double prefix = 0.0;
+  // The serial binary64 prefix sums in candidate order, one pass: lane j
+  // keeps prefix_j = (..((w_0 + w_1) + w_2) ..) + w_j; the total is the last.
+  double prefix = 0.0, pre_j = 0.0;
   for (int j = 0; j < c; ++j) {
     prefix = prefix + lane_f64(w, j);
-    if (prefix >= thr) {
-      n = j + 1;
-      break;
-    }
+    pre_j = lane == j ? prefix : pre_j;
   }
-  // min-p relative to w_0 = 1
+  // top-p: the first n with prefix_{n-1} >= top_p * total
+  const double thr = P.top_p * prefix;
+  const uint64_t reach = __ballot(in && pre_j >= thr);
+  int n = reach ? (int)__builtin_ctzll(reach) + 1 : c;
+  // min-p relative to w_0 = 1: the first j >= 1 with w_j < min_p ends it
   if (P.min_p > 0.0) {
-    int m = 1;
-    while (m < n && lane_f64(w, m) >= P.min_p) ++m;
-    n = m;
+    const uint64_t below = __ballot(lane >= 1 && lane < n && w < P.min_p);
+    if (below) n = (int)__builtin_ctzll(below);
   }
   int pick = n - 1;
   if (P.version == YSKN_V3) {
     // argmax of z + g over the retained candidates; the earliest wins ties
-    double best = lane < n ? sc : -__builtin_inf();
-    int bj = lane < n ? lane : 64;
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) {
-      const double ob = __shfl_xor(best, o);
-      const int oj = __shfl_xor(bj, o);
-      if (ob > best || (ob == best && oj < bj)) {
-        best = ob;
-        bj = oj;
-      }
+    // (order-preserving 64-bit keys of the scores, -0 taken as +0)
+    uint64_t key = 0ull;
+    if (lane < n) {
+      const uint64_t b = (uint64_t)__double_as_longlong(sc == 0.0 ? 0.0 : sc);
+      key = (b >> 63) ? ~b : (b | 0x8000000000000000ull);
     }
-    if (bj < n) pick = bj;
+    const uint64_t best = wave_max_u64_dpp(key);
+    const uint64_t hit = __ballot(lane < n && key == best);
+    if (hit) pick = (int)__builtin_ctzll(hit);
   } else {
-    double mass = 0.0;
-    for (int j = 0; j < n; ++j) mass = mass + lane_f64(w, j);
+    // the retained mass is prefix_{n-1} (the same serial sum); the first
+    // j with t < prefix_j is drawn
+    const double mass = lane_f64(pre_j, n - 1);
     const double t = uniform_v2(P.seed, pos) * mass;
-    double pre = 0.0;
-    for (int j = 0; j < n; ++j) {
-      pre = pre + lane_f64(w, j);
-      if (t < pre) {
-        pick = j;
-        break;
-      }
-    }
+    const uint64_t hit = __ballot(lane < n && t < pre_j);
+    if (hit) pick = (int)__builtin_ctzll(hit);
   }
   const uint32_t id = pk_id((uint64_t)(((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(cj >> 32), pick) << 32) |
                                        (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)cj, pick)));
@@ -1191,69 +1235,87 @@ __global__ __launch_bounds__(NT) void smp_row(SmpArgs A) {
   // above the list's last value, which is therefore a valid top-KB bound).
   // Waves share the best such bound and the row maximum through LDS atomics;
   // nothing in the stream waits for another wave.
-  uint32_t lst = 0u, theta_w = 0u, q_pub = 0u;
+  // A lane maximum at or below the row's certified bound th_row cannot be
+  // among the row's top KB and does not enter the list: any KB distinct
+  // elements certify their smallest value as a bound, so the lists stay
+  // valid while the row bound filters what reaches them.
+  uint32_t lst = 0u, theta_w = 0u, q_pub = 0u, th_row = 0u;
   const int qidx = (plan.KB + NW - 1) / NW - 1;
   // per chunk: its r largest lane maxima enter the list (the first chunk: up
   // to KB of them, so the bound exists from the start)
   const int r_first = plan.KB < 64 ? plan.KB : 64;
   const int r_next = plan.KB < 8 ? plan.KB : 8;
 
+  // Below lo_f nothing can matter to this wave: no lane maximum would enter
+  // its list (lo_f <= its KB-th value), no value would be a candidate
+  // (lo_f <= the threshold it last used) or a mass term (lo_f <= m_ref -
+  // ZMASS). A chunk whose values all lie below it costs its conversion and
+  // one comparison; the bounds only rise, so a stale lo_f is merely low.
+  float lo_f = -__builtin_inff();
+
   // one chunk: c from X; in the stream, prefetch the wave's chunk two steps
   // ahead into X
   auto step = [&](uint32_t (&X)[EPT], int c, bool first, bool stream) {
     float lmax = -__builtin_inff();
     chunk_values<DT, PEN>(rc, V, c, lane, X, lmax, ws.bad);
-    uint32_t lk = lmax == -__builtin_inff() ? 0u : f2key(__float_as_uint(lmax));
-    uint32_t cmax = 0u;
-    const int rr = first ? r_first : r_next;
-    for (int i = 0; i < rr; ++i) {
-      const uint32_t m = wave_max_dpp(lk);
-      if (i == 0) cmax = m;
-      if (m <= theta_w) break;  // 0, or cannot enter the full list
-      // insert m: entries >= m keep their lanes, the rest move up by one
-      const uint32_t pos = (uint32_t)__popcll(__ballot(lane < plan.KB && lst >= m));
-      const uint32_t up = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)lst, 0x138, 0xf, 0xf, false);  // wave_shr:1
-      lst = (uint32_t)lane < pos ? lst : ((uint32_t)lane == pos ? m : up);
-      theta_w = (uint32_t)__builtin_amdgcn_readlane((int)lst, plan.KB - 1);
-      const uint64_t eq = __ballot(lk == m);
-      if (lane == (int)__builtin_ctzll(eq)) lk = 0u;
-    }
-    if (cmax > ws.wkey) {
-      ws.wkey = cmax;
-      if (lane == 0) atomicMax(&sh.mkey, cmax);
-    }
-    // Two certified bounds: the best single wave's KB-th value, and the
-    // minimum over the waves of their ceil(KB/8)-th values (each wave has
-    // that many elements at or above it: 8 * ceil(KB/8) >= KB in all).
-    uint32_t th = (uint32_t)__builtin_amdgcn_readfirstlane(
-        __hip_atomic_load(&sh.theta, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP));
-    if (theta_w > th) {
-      if (lane == 0) atomicMax(&sh.theta, theta_w);
-      th = theta_w;
-    }
-    {
-      const uint32_t qw = (uint32_t)__builtin_amdgcn_readlane((int)lst, qidx);
-      if (qw > q_pub) {
-        q_pub = qw;
-        if (lane == 0) __hip_atomic_store(&sh.q[wave], qw, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    if (first || __ballot(lmax >= lo_f)) {
+      uint32_t lk = lmax == -__builtin_inff() ? 0u : f2key(__float_as_uint(lmax));
+      uint32_t cmax = 0u;
+      const int rr = first ? r_first : r_next;
+      for (int i = 0; i < rr; ++i) {
+        const uint32_t m = wave_max_dpp(lk);
+        if (i == 0) cmax = m;
+        if (m <= theta_w || m <= th_row) break;  // 0, cannot enter the full list, or below the row bound
+        // insert m: entries >= m keep their lanes, the rest move up by one
+        const uint32_t pos = (uint32_t)__popcll(__ballot(lane < plan.KB && lst >= m));
+        const uint32_t up = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)lst, 0x138, 0xf, 0xf, false);  // wave_shr:1
+        lst = (uint32_t)lane < pos ? lst : ((uint32_t)lane == pos ? m : up);
+        theta_w = (uint32_t)__builtin_amdgcn_readlane((int)lst, plan.KB - 1);
+        const uint64_t eq = __ballot(lk == m);
+        if (lane == (int)__builtin_ctzll(eq)) lk = 0u;
       }
-      uint32_t qmin = lane < NW ? __hip_atomic_load(&sh.q[lane], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP)
-                                : 0xffffffffu;
-      qmin = (uint32_t)__builtin_amdgcn_readfirstlane((int)wave_min_u32_dpp(qmin));
-      th = qmin > th ? qmin : th;
+      if (cmax > ws.wkey) {
+        ws.wkey = cmax;
+        if (lane == 0) atomicMax(&sh.mkey, cmax);
+      }
+      // Two certified bounds: the best single wave's KB-th value, and the
+      // minimum over the waves of their ceil(KB/8)-th values (each wave has
+      // that many elements at or above it: 8 * ceil(KB/8) >= KB in all).
+      uint32_t th = (uint32_t)__builtin_amdgcn_readfirstlane(
+          __hip_atomic_load(&sh.theta, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP));
+      if (theta_w > th) {
+        if (lane == 0) atomicMax(&sh.theta, theta_w);
+        th = theta_w;
+      }
+      {
+        const uint32_t qw = (uint32_t)__builtin_amdgcn_readlane((int)lst, qidx);
+        if (qw > q_pub) {
+          q_pub = qw;
+          if (lane == 0) __hip_atomic_store(&sh.q[wave], qw, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+        }
+        uint32_t qmin = lane < NW ? __hip_atomic_load(&sh.q[lane], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP)
+                                  : 0xffffffffu;
+        qmin = (uint32_t)__builtin_amdgcn_readfirstlane((int)wave_min_u32_dpp(qmin));
+        th = qmin > th ? qmin : th;
+      }
+      // the row maximum as LDS holds it (a workgroup-scope atomic read: a
+      // volatile access through a generic pointer would become a flat load
+      // that waits for every outstanding global load -- the prefetch)
+      uint32_t mk = (uint32_t)__builtin_amdgcn_readfirstlane(
+          __hip_atomic_load(&sh.mkey, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP));
+      mk = mk > ws.wkey ? mk : ws.wkey;
+      const uint32_t thr = A.force_dense ? 0xffffffffu : row_threshold(plan, P, key2f(mk), th);
+      // (a wave's first chunk has about KB lanes with survivors by
+      // construction -- the lane maxima that set its first bound -- so its
+      // deferral limit is raised by KB)
+      chunk_filter<DT>(c, lane, X, thr, mk, A.want_mass != 0, cmax, first ? DLANES + plan.KB : DLANES, ws, sh,
+                       fl, spill);
+      th_row = th;
+      const float lo_list = key_threshold_float(theta_w > th ? theta_w : th);
+      const float lo_cand = key_threshold_float(thr);
+      const float lo_mass = A.want_mass ? ws.m_ref - ZMASS : __builtin_inff();
+      lo_f = mk == 0u ? -__builtin_inff() : fminf(fminf(lo_list, lo_cand), lo_mass);
     }
-    // the row maximum as LDS holds it (a workgroup-scope atomic read: a
-    // volatile access through a generic pointer would become a flat load
-    // that waits for every outstanding global load -- the prefetch)
-    uint32_t mk = (uint32_t)__builtin_amdgcn_readfirstlane(
-        __hip_atomic_load(&sh.mkey, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP));
-    mk = mk > ws.wkey ? mk : ws.wkey;
-    const uint32_t thr = A.force_dense ? 0xffffffffu : row_threshold(plan, P, key2f(mk), th);
-    // (a wave's first chunk has about KB lanes with survivors by
-    // construction -- the lane maxima that set its first bound -- so its
-    // deferral limit is raised by KB)
-    chunk_filter<DT>(c, lane, X, thr, mk, A.want_mass != 0, cmax, first ? DLANES + plan.KB : DLANES, ws, sh,
-                     fl, spill);
     if (stream) load_full<DT>(rc.base, V, c + 2 * NW, c + 2 * NW < nfull, lane, X);
   };
   // pairs of steps with no condition between them: at every step the buffer
@@ -1278,13 +1340,8 @@ __global__ __launch_bounds__(NT) void smp_row(SmpArgs A) {
   if (lane < 8) fl.lists[wave * 8 + lane] = lane < plan.KB ? lst : 0u;
   __syncthreads();  // every append, deferral, list and maximum is in LDS
   if (wave == 0) {
-    const uint32_t x = fl.lists[lane];
-    uint32_t rank = 0;
-    for (int j = 0; j < 64; ++j) {
-      const uint32_t y = (uint32_t)__builtin_amdgcn_readlane((int)x, j);
-      rank += (y > x || (y == x && j < lane)) ? 1u : 0u;
-    }
-    if (x != 0u && rank == (uint32_t)(plan.KB - 1)) atomicMax(&sh.theta, x);
+    const uint32_t t = wave_kth_largest_radix(fl.lists[lane], plan.KB);
+    if (lane == 0 && t != 0u) atomicMax(&sh.theta, t);
   }
   __syncthreads();
   const uint32_t theta = sh.theta;
@@ -1325,7 +1382,7 @@ __global__ __launch_bounds__(NT) void smp_row(SmpArgs A) {
   }
   if (__ballot(ws.bad)) wflags |= F_NONFINITE;
   {
-    const double wm = A.want_mass ? wave_sum_f64(ws.acc) : 0.0;
+    const double wm = A.want_mass ? wave_sum_f64_dpp(ws.acc) : 0.0;
     if (lane == 0) {
       if (wflags) atomicOr(&sh.flags, wflags);
       s_mref[wave] = ws.m_ref;
@@ -1342,7 +1399,7 @@ __global__ __launch_bounds__(NT) void smp_row(SmpArgs A) {
     // one term per wave, in lanes 0..NW-1 of every wave
     double t = 0.0;
     if (lane < NW && s_mref[lane] != -__builtin_inff()) t = s_mass[lane] * exp((double)s_mref[lane] - (double)M);
-    logZ = log(wave_sum_f64(t));
+    logZ = log(wave_sum_f64_dpp(t));
   }
   int32_t status = ST_OK;
   if (rflags & F_INVALID) status = ST_EINVAL;
