@@ -1023,31 +1023,27 @@ struct WaveState {
 };
 
 // Shared streaming state of a row block.
-struct RowShared {
-  uint32_t count;   // entries appended (beyond BUFCAP they went to the spill area)
-  uint32_t mkey;    // running row maximum key
-  uint32_t flags;   // F_* of the row
-  uint32_t theta;   // best top-KB bound any wave has certified
-  uint32_t q[NW];   // per wave: the ceil(KB/8)-th value of its list
-  uint32_t ndef;    // deferred chunks recorded (may exceed DEFCAP: those were not deferred)
-  uint32_t ctr;     // compaction counter
-};
+// The bounds the waves share sit in one array so that a wave reads all of
+// them with a single LDS load (lane i reads word i).
+constexpr int BW_THETA = 0;       // best top-KB bound any wave has certified
+constexpr int BW_Q = 1;           // BW_Q + w: wave w's ceil(KB/8)-th list value
+constexpr int BW_MKEY = 1 + NW;   // running row maximum key
+constexpr int BW_N = 2 + NW;
+static_assert(BW_N <= 16, "the shared bounds are read by the lanes of one DPP row");
 
-// Wave maximum of the chunk just converted; the row maximum in LDS follows.
-__device__ __forceinline__ void chunk_max(float lmax, WaveState& ws, RowShared& sh) {
-  const uint32_t lk = lmax == -__builtin_inff() ? 0u : f2key(__float_as_uint(lmax));
-  const uint32_t wm = wave_max_dpp(lk);
-  if (wm > ws.wkey) {
-    ws.wkey = wm;
-    if ((threadIdx.x & 63) == 0) atomicMax(&sh.mkey, wm);
-  }
-}
+struct RowShared {
+  uint32_t count;      // entries appended (beyond BUFCAP they went to the spill area)
+  uint32_t flags;      // F_* of the row
+  uint32_t bw[BW_N];   // shared bounds (BW_*)
+  uint32_t ndef;       // deferred chunks recorded (may exceed DEFCAP: those were not deferred)
+  uint32_t ctr;        // compaction counter
+};
 
 // Mass terms (if mass) and candidates of chunk c for threshold thr. Work is
 // skipped per chunk (its maximum), then per load group (GRP consecutive
 // values of a lane), then per element slot, wherever no lane holds a value
-// >= min(threshold, m_ref - ZMASS); survivors reserve their slots with one
-// LDS atomic per element slot that has any. Mass terms are binary32
+// >= min(threshold, m_ref - ZMASS); the chunk's survivors are counted first
+// and reserve their slots with one LDS atomic. Mass terms are binary32
 // exponentials accumulated in binary64: next to the row maximum's term (1.0)
 // the small terms must not be rounded away, since the top token's logprob is
 // -log(1 + their sum). Slots beyond BUFCAP go to the row's spill area in
@@ -1100,37 +1096,48 @@ __device__ __forceinline__ void chunk_filter(int c, int lane, const uint32_t (&k
     }
   }
   const uint32_t eb = (uint32_t)c * WSEG + (uint32_t)lane * GRP;
-  bool spilled = false;
+  // pass 1: mass terms, and the number of candidates of the chunk
+  uint32_t nk = 0u;
 #pragma unroll
   for (int q = 0; q < NGRP; ++q) {
     if (!__ballot(gmax[q] >= tany)) continue;
 #pragma unroll
     for (int j = 0; j < GRP; ++j) {
-      const int i = q * GRP + j;
-      const float v = __uint_as_float(kb[i]);
+      const float v = __uint_as_float(kb[q * GRP + j]);
       if (!__ballot(v >= tany)) continue;
       if (v >= lo) ws.acc += (double)__builtin_amdgcn_exp2f((v - ws.m_ref) * 1.4426950408889634f);
-      if (keep_any) {
-        const bool k = v >= thf;
-        const uint64_t km = __ballot(k);
-        if (km) {
-          const int first = (int)__builtin_ctzll(km);
-          uint32_t base = 0;
-          if (lane == first) base = atomicAdd(&sh.count, (uint32_t)__popcll(km));
-          base = (uint32_t)__builtin_amdgcn_readlane((int)base, first);
-          const uint32_t slot = base + lanes_below(km);
-          const uint64_t e = pack(f2key(__float_as_uint(v)), eb + (uint32_t)(q * 64 * GRP + j));
-          if (base + (uint32_t)__popcll(km) <= (uint32_t)BUFCAP) {
-            if (k) ((lds_u64*)fl.buf)[slot] = e;
-          } else {
-            // rare: the buffer is full; below BUFCAP to LDS, the rest to
-            // the spill area
-            if (k && slot < (uint32_t)BUFCAP) ((lds_u64*)fl.buf)[slot] = e;
-            if (k && slot >= (uint32_t)BUFCAP) __builtin_nontemporal_store(e, &((global_u64*)spill)[slot - BUFCAP]);
-            spilled = true;
-          }
-        }
+      if (keep_any) nk += (uint32_t)__popcll(__ballot(v >= thf));
+    }
+  }
+  if (nk == 0u) return;
+  // pass 2: one LDS atomic reserves the chunk's slots; the candidates are
+  // written in (group, element, lane) order
+  uint32_t base = 0u;
+  if (lane == 0) base = atomicAdd(&sh.count, nk);
+  base = (uint32_t)__builtin_amdgcn_readfirstlane((int)base);
+  const bool fits = base + nk <= (uint32_t)BUFCAP;
+  bool spilled = false;
+#pragma unroll
+  for (int q = 0; q < NGRP; ++q) {
+    if (!__ballot(gmax[q] >= thf)) continue;
+#pragma unroll
+    for (int j = 0; j < GRP; ++j) {
+      const float v = __uint_as_float(kb[q * GRP + j]);
+      const bool k = v >= thf;
+      const uint64_t km = __ballot(k);
+      if (!km) continue;
+      const uint32_t slot = base + lanes_below(km);
+      const uint64_t e = pack(f2key(__float_as_uint(v)), eb + (uint32_t)(q * 64 * GRP + j));
+      if (fits) {
+        if (k) ((lds_u64*)fl.buf)[slot] = e;
+      } else {
+        // rare: the buffer is full; below BUFCAP to LDS, the rest to the
+        // spill area
+        if (k && slot < (uint32_t)BUFCAP) ((lds_u64*)fl.buf)[slot] = e;
+        if (k && slot >= (uint32_t)BUFCAP) __builtin_nontemporal_store(e, &((global_u64*)spill)[slot - BUFCAP]);
+        spilled = true;
       }
+      base += (uint32_t)__popcll(km);
     }
   }
   if (spilled) __builtin_amdgcn_s_waitcnt(0);
@@ -1204,14 +1211,10 @@ __global__ __launch_bounds__(NT) void smp_row(SmpArgs A) {
   const int nch = (V + WSEG - 1) / WSEG;
   if (tid == 0) {
     sh.count = 0u;
-    sh.mkey = 0u;
     sh.flags = 0u;
-    sh.theta = 0u;
     sh.ndef = 0u;
   }
-  if (tid < NW) {
-    sh.q[tid] = 0u;
-  }
+  if (tid < BW_N) sh.bw[tid] = 0u;
   uint64_t* const spill = A.dense_b + (int64_t)row * A.dense_ld;
 
   WaveState ws;
@@ -1240,6 +1243,8 @@ __global__ __launch_bounds__(NT) void smp_row(SmpArgs A) {
   // elements certify their smallest value as a bound, so the lists stay
   // valid while the row bound filters what reaches them.
   uint32_t lst = 0u, theta_w = 0u, q_pub = 0u, th_row = 0u;
+  uint32_t thr_mk = 0u, thr_th = 0u, thr_c = 1u;  // the last row threshold and its inputs
+  uint32_t theta_pub = 0u;                          // theta_w as last published
   const int qidx = (plan.KB + NW - 1) / NW - 1;
   // per chunk: its r largest lane maxima enter the list (the first chunk: up
   // to KB of them, so the bound exists from the start)
@@ -1276,35 +1281,54 @@ __global__ __launch_bounds__(NT) void smp_row(SmpArgs A) {
       }
       if (cmax > ws.wkey) {
         ws.wkey = cmax;
-        if (lane == 0) atomicMax(&sh.mkey, cmax);
+        if (lane == 0) atomicMax(&sh.bw[BW_MKEY], cmax);
       }
-      // Two certified bounds: the best single wave's KB-th value, and the
-      // minimum over the waves of their ceil(KB/8)-th values (each wave has
-      // that many elements at or above it: 8 * ceil(KB/8) >= KB in all).
-      uint32_t th = (uint32_t)__builtin_amdgcn_readfirstlane(
-          __hip_atomic_load(&sh.theta, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP));
-      if (theta_w > th) {
-        if (lane == 0) atomicMax(&sh.theta, theta_w);
-        th = theta_w;
+      if (theta_w > theta_pub) {
+        // every bound a wave uses must reach the shared one: the final
+        // bound is taken from it and may not be lower
+        theta_pub = theta_w;
+        if (lane == 0) atomicMax(&sh.bw[BW_THETA], theta_w);
       }
       {
         const uint32_t qw = (uint32_t)__builtin_amdgcn_readlane((int)lst, qidx);
         if (qw > q_pub) {
           q_pub = qw;
-          if (lane == 0) __hip_atomic_store(&sh.q[wave], qw, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+          if (lane == 0) atomicMax(&sh.bw[BW_Q + wave], qw);
         }
-        uint32_t qmin = lane < NW ? __hip_atomic_load(&sh.q[lane], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP)
-                                  : 0xffffffffu;
-        qmin = (uint32_t)__builtin_amdgcn_readfirstlane((int)wave_min_u32_dpp(qmin));
-        th = qmin > th ? qmin : th;
       }
-      // the row maximum as LDS holds it (a workgroup-scope atomic read: a
-      // volatile access through a generic pointer would become a flat load
-      // that waits for every outstanding global load -- the prefetch)
-      uint32_t mk = (uint32_t)__builtin_amdgcn_readfirstlane(
-          __hip_atomic_load(&sh.mkey, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP));
+      // Every shared bound in one LDS load (a workgroup-scope atomic read:
+      // a volatile access through a generic pointer would become a flat load
+      // that waits for every outstanding global load -- the prefetch). Two
+      // certified bounds: the best single wave's KB-th value, and the minimum
+      // over the waves of their ceil(KB/8)-th values (each wave has that many
+      // elements at or above it: 8 * ceil(KB/8) >= KB in all).
+      const uint32_t bw = lane < BW_N ? __hip_atomic_load(&sh.bw[lane], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP)
+                                      : 0u;
+      uint32_t qv = (lane >= BW_Q && lane < BW_Q + NW) ? bw : 0xffffffffu;
+      {
+        uint32_t t;
+        t = (uint32_t)__builtin_amdgcn_update_dpp(-1, (int)qv, 0x111, 0xf, 0xf, false);  // row_shr:1
+        qv = qv < t ? qv : t;
+        t = (uint32_t)__builtin_amdgcn_update_dpp(-1, (int)qv, 0x112, 0xf, 0xf, false);  // row_shr:2
+        qv = qv < t ? qv : t;
+        t = (uint32_t)__builtin_amdgcn_update_dpp(-1, (int)qv, 0x114, 0xf, 0xf, false);  // row_shr:4
+        qv = qv < t ? qv : t;
+        t = (uint32_t)__builtin_amdgcn_update_dpp(-1, (int)qv, 0x118, 0xf, 0xf, false);  // row_shr:8
+        qv = qv < t ? qv : t;
+      }
+      const uint32_t qmin = (uint32_t)__builtin_amdgcn_readlane((int)qv, 15);
+      uint32_t th = (uint32_t)__builtin_amdgcn_readlane((int)bw, BW_THETA);
+      th = th > theta_w ? th : theta_w;
+      th = qmin > th ? qmin : th;
+      uint32_t mk = (uint32_t)__builtin_amdgcn_readlane((int)bw, BW_MKEY);
       mk = mk > ws.wkey ? mk : ws.wkey;
-      const uint32_t thr = A.force_dense ? 0xffffffffu : row_threshold(plan, P, key2f(mk), th);
+      // the row threshold changes only with (mk, th): computed again only then
+      if (mk != thr_mk || th != thr_th) {
+        thr_mk = mk;
+        thr_th = th;
+        thr_c = A.force_dense ? 0xffffffffu : row_threshold(plan, P, key2f(mk), th);
+      }
+      const uint32_t thr = thr_c;
       // (a wave's first chunk has about KB lanes with survivors by
       // construction -- the lane maxima that set its first bound -- so its
       // deferral limit is raised by KB)
@@ -1335,21 +1359,21 @@ __global__ __launch_bounds__(NT) void smp_row(SmpArgs A) {
   // A final bound from the union of the waves' lists: the KB-th largest of
   // their top 8 entries (64 distinct elements, ranked by one wave). It is at
   // least the minimum over the waves of their ceil(KB/8)-th values, and
-  // sh.theta keeps the best single-wave bound: no bound used in the stream
+  // sh.bw[BW_THETA] keeps the best single-wave bound: no bound used in the stream
   // exceeds the final one, which keeps the buffer complete down to it.
   if (lane < 8) fl.lists[wave * 8 + lane] = lane < plan.KB ? lst : 0u;
   __syncthreads();  // every append, deferral, list and maximum is in LDS
   if (wave == 0) {
     const uint32_t t = wave_kth_largest_radix(fl.lists[lane], plan.KB);
-    if (lane == 0 && t != 0u) atomicMax(&sh.theta, t);
+    if (lane == 0 && t != 0u) atomicMax(&sh.bw[BW_THETA], t);
   }
   __syncthreads();
-  const uint32_t theta = sh.theta;
+  const uint32_t theta = sh.bw[BW_THETA];
   // deferred chunks whose largest key reaches the final bound: read again
   // and filter with that bound. Entry i belongs to wave i % NW; each wave
   // keeps two of its chunks in flight (the stream's buffers are free now).
   if (!A.force_dense) {
-    const uint32_t mkf = sh.mkey;
+    const uint32_t mkf = sh.bw[BW_MKEY];
     const uint32_t thr_f = row_threshold(plan, P, key2f(mkf), theta);
     const uint32_t nd = sh.ndef < (uint32_t)DEFCAP ? sh.ndef : (uint32_t)DEFCAP;
     auto next = [&](uint32_t from) -> uint32_t {
@@ -1392,7 +1416,7 @@ __global__ __launch_bounds__(NT) void smp_row(SmpArgs A) {
   __syncthreads();
 
   // ---- row results -----------------------------------------------------
-  const float M = key2f(sh.mkey);
+  const float M = key2f(sh.bw[BW_MKEY]);
   const uint32_t rflags = sh.flags;
   double logZ = 0.0;
   if (A.want_mass) {
