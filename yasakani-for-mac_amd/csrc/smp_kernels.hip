@@ -528,19 +528,27 @@ __device__ __forceinline__ double lane_f64(double x, int j) {
   return __longlong_as_double((long long)(((uint64_t)hi << 32) | lo));
 }
 
+// With `have_pre`, pre[j] and pre[64 + j] already hold candidate j's weight
+// and (version 3) score, computed by other waves while the candidates were
+// being ranked.
 __device__ __forceinline__ void sample_tail_wave(const SmpArgs& A, const DevParams& P, int row,
-                                                 const uint64_t* cand, int c) {
+                                                 const uint64_t* cand, int c, uint64_t pos, const double* pre,
+                                                 bool have_pre) {
   const int lane = threadIdx.x & 63;
   const double T = P.temperature;
   const float v0 = key2f(pk_key(cand[0]));
-  const uint64_t pos = position_of(A, row, 0);
   const bool in = lane < c;
   const uint64_t cj = in ? cand[lane] : 0ull;
-  double z = 0.0, w = 0.0, sc = -__builtin_inf();
+  double w = 0.0, sc = -__builtin_inf();
   if (in) {
-    z = ((double)key2f(pk_key(cj)) - (double)v0) / T;  // widen, subtract, divide
-    w = exp_d(z);
-    if (P.version == YSKN_V3) sc = z + gumbel_from_key(position_key(P.seed, pos), pk_id(cj));
+    if (have_pre) {
+      w = pre[lane];
+      if (P.version == YSKN_V3) sc = pre[64 + lane];
+    } else {
+      const double z = ((double)key2f(pk_key(cj)) - (double)v0) / T;  // widen, subtract, divide
+      w = exp_d_inline(z);
+      if (P.version == YSKN_V3) sc = z + gumbel_from_key<true>(position_key(P.seed, pos), pk_id(cj));
+    }
   }
   // The serial binary64 prefix sums in candidate order, one pass: lane j
   // keeps prefix_j = (..((w_0 + w_1) + w_2) ..) + w_j; the total is the last.
@@ -881,8 +889,8 @@ struct RowLds {
   uint64_t buf[BUFCAP];    // append buffer of candidates (unordered)
   uint64_t cand[CAP];      // the candidates that pass the final bounds, sorted
   double w[CAP];           // weights of the tail; scratch of the sorts
-  uint32_t lists[NW * KBMAX];  // the waves' top-KB lists, merged after the stream
   uint2 def[DEFCAP];           // deferred chunks: (chunk, its largest key)
+  uint32_t lists[NW * 8];      // each wave's 8 largest list entries, after the stream
 };
 
 // Raw bits of chunk c (2,048 logits) of a row into kb; nothing for c >= nch.
@@ -1199,6 +1207,10 @@ __global__ __launch_bounds__(NT) void smp_row(SmpArgs A) {
   __shared__ float s_mref[NW];
   __shared__ double s_mass[NW];
   __shared__ TailShared ts;
+  __shared__ uint64_t s_pos;       // position of the row's first draw
+  __shared__ uint32_t s_rank[64];  // ranks of up to 64 final candidates
+  __shared__ double s_wpre[64];    // their weights, in compaction order
+  __shared__ double s_spre[64];    // their version-3 scores, in compaction order
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -1215,6 +1227,8 @@ __global__ __launch_bounds__(NT) void smp_row(SmpArgs A) {
     sh.ndef = 0u;
   }
   if (tid < BW_N) sh.bw[tid] = 0u;
+  if (tid < 64) s_rank[tid] = 0u;
+  if (tid == 64) sh.ctr = 0u;
   uint64_t* const spill = A.dense_b + (int64_t)row * A.dense_ld;
 
   WaveState ws;
@@ -1356,54 +1370,19 @@ __global__ __launch_bounds__(NT) void smp_row(SmpArgs A) {
     load_chunk<DT, VEC>(rc, V, nch, c, lane, buf0);
     step(buf0, c, c == wave, false);
   }
+  // The first draw's position: a global load waits behind the other rows'
+  // streams (microseconds), so it is read here, by the last wave, which
+  // has the fewest chunks and would wait at the barrier below anyway.
+  if (tid == (NW - 1) * 64 && A.out_ids != nullptr) s_pos = position_of(A, row, 0);
   // A final bound from the union of the waves' lists: the KB-th largest of
-  // their top 8 entries (64 distinct elements, ranked by one wave). It is at
-  // least the minimum over the waves of their ceil(KB/8)-th values, and
-  // sh.bw[BW_THETA] keeps the best single-wave bound: no bound used in the stream
-  // exceeds the final one, which keeps the buffer complete down to it.
+  // their top 8 entries (64 distinct elements). It is at least the minimum
+  // over the waves of their ceil(KB/8)-th values, and sh.bw[BW_THETA] keeps
+  // the best single-wave bound: no bound used in the stream exceeds the
+  // final one (every improvement was published), which keeps the buffer
+  // complete down to it.
   if (lane < 8) fl.lists[wave * 8 + lane] = lane < plan.KB ? lst : 0u;
-  __syncthreads();  // every append, deferral, list and maximum is in LDS
-  if (wave == 0) {
-    const uint32_t t = wave_kth_largest_radix(fl.lists[lane], plan.KB);
-    if (lane == 0 && t != 0u) atomicMax(&sh.bw[BW_THETA], t);
-  }
-  __syncthreads();
-  const uint32_t theta = sh.bw[BW_THETA];
-  // deferred chunks whose largest key reaches the final bound: read again
-  // and filter with that bound. Entry i belongs to wave i % NW; each wave
-  // keeps two of its chunks in flight (the stream's buffers are free now).
-  if (!A.force_dense) {
-    const uint32_t mkf = sh.bw[BW_MKEY];
-    const uint32_t thr_f = row_threshold(plan, P, key2f(mkf), theta);
-    const uint32_t nd = sh.ndef < (uint32_t)DEFCAP ? sh.ndef : (uint32_t)DEFCAP;
-    auto next = [&](uint32_t from) -> uint32_t {
-      for (uint32_t i = from; i < nd; i += NW)
-        if (fl.def[i].y >= thr_f) return i;
-      return nd;
-    };
-    auto redo = [&](uint32_t (&X)[EPT], uint32_t i) {
-      const int cc = (int)fl.def[i].x;
-      float lmax = -__builtin_inff();
-      bool bad = false;
-      chunk_values<DT, PEN>(rc, V, cc, lane, X, lmax, bad);
-      chunk_filter<DT>(cc, lane, X, thr_f, mkf, false, fl.def[i].y, 64, ws, sh, fl, spill);
-    };
-    uint32_t ia = next((uint32_t)wave);
-    uint32_t ib = ia < nd ? next(ia + NW) : nd;
-    if (ia < nd) load_chunk<DT, VEC>(rc, V, nch, (int)fl.def[ia].x, lane, buf0);
-    if (ib < nd) load_chunk<DT, VEC>(rc, V, nch, (int)fl.def[ib].x, lane, buf1);
-    while (ia < nd) {
-      redo(buf0, ia);
-      const uint32_t ic = ib < nd ? next(ib + NW) : nd;
-      if (ic < nd) load_chunk<DT, VEC>(rc, V, nch, (int)fl.def[ic].x, lane, buf0);
-      if (ib >= nd) break;
-      redo(buf1, ib);
-      const uint32_t id = ic < nd ? next(ic + NW) : nd;
-      if (id < nd) load_chunk<DT, VEC>(rc, V, nch, (int)fl.def[id].x, lane, buf1);
-      ia = ic;
-      ib = id;
-    }
-  }
+  // The wave's own results, which the deferred reads below do not change
+  // (they add no mass terms and find no new maximum).
   if (__ballot(ws.bad)) wflags |= F_NONFINITE;
   {
     const double wm = A.want_mass ? wave_sum_f64_dpp(ws.acc) : 0.0;
@@ -1413,18 +1392,58 @@ __global__ __launch_bounds__(NT) void smp_row(SmpArgs A) {
       s_mass[wave] = wm;
     }
   }
-  __syncthreads();
+  __syncthreads();  // every append, deferral, list, maximum and mass term is in LDS
+  // every wave ranks the union itself (the same value in all): no second barrier
+  uint32_t theta = sh.bw[BW_THETA];
+  {
+    const uint32_t t = wave_kth_largest_radix(fl.lists[lane], plan.KB);
+    theta = t > theta ? t : theta;
+  }
+  // deferred chunks whose largest key reaches the final bound: read again
+  // and filter with that bound. Entry i belongs to wave i % NW; each wave
+  // keeps two of its chunks in flight (the stream's buffers are free now).
+  if (!A.force_dense) {
+    const uint32_t mkf = sh.bw[BW_MKEY];
+    const uint32_t thr_f = row_threshold(plan, P, key2f(mkf), theta);
+    const uint32_t nd = sh.ndef < (uint32_t)DEFCAP ? sh.ndef : (uint32_t)DEFCAP;
+    // (every wave sees the same entries: the condition is block-uniform)
+    bool any = false;
+    for (uint32_t i = (uint32_t)lane; i < nd; i += 64) any = any || fl.def[i].y >= thr_f;
+    if (__ballot(any)) {
+      auto next = [&](uint32_t from) -> uint32_t {
+        for (uint32_t i = from; i < nd; i += NW)
+          if (fl.def[i].y >= thr_f) return i;
+        return nd;
+      };
+      auto redo = [&](uint32_t (&X)[EPT], uint32_t i) {
+        const int cc = (int)fl.def[i].x;
+        float lmax = -__builtin_inff();
+        bool bad = false;
+        chunk_values<DT, PEN>(rc, V, cc, lane, X, lmax, bad);
+        chunk_filter<DT>(cc, lane, X, thr_f, mkf, false, fl.def[i].y, 64, ws, sh, fl, spill);
+      };
+      uint32_t ia = next((uint32_t)wave);
+      uint32_t ib = ia < nd ? next(ia + NW) : nd;
+      if (ia < nd) load_chunk<DT, VEC>(rc, V, nch, (int)fl.def[ia].x, lane, buf0);
+      if (ib < nd) load_chunk<DT, VEC>(rc, V, nch, (int)fl.def[ib].x, lane, buf1);
+      while (ia < nd) {
+        redo(buf0, ia);
+        const uint32_t ic = ib < nd ? next(ib + NW) : nd;
+        if (ic < nd) load_chunk<DT, VEC>(rc, V, nch, (int)fl.def[ic].x, lane, buf0);
+        if (ib >= nd) break;
+        redo(buf1, ib);
+        const uint32_t id = ic < nd ? next(ic + NW) : nd;
+        if (id < nd) load_chunk<DT, VEC>(rc, V, nch, (int)fl.def[id].x, lane, buf1);
+        ia = ic;
+        ib = id;
+      }
+      __syncthreads();  // the deferred chunks' appends are in LDS
+    }
+  }
 
   // ---- row results -----------------------------------------------------
   const float M = key2f(sh.bw[BW_MKEY]);
   const uint32_t rflags = sh.flags;
-  double logZ = 0.0;
-  if (A.want_mass) {
-    // one term per wave, in lanes 0..NW-1 of every wave
-    double t = 0.0;
-    if (lane < NW && s_mref[lane] != -__builtin_inff()) t = s_mass[lane] * exp((double)s_mref[lane] - (double)M);
-    logZ = log(wave_sum_f64_dpp(t));
-  }
   int32_t status = ST_OK;
   if (rflags & F_INVALID) status = ST_EINVAL;
   else if (rflags & F_NONFINITE) status = ST_ENONFINITE;
@@ -1438,33 +1457,66 @@ __global__ __launch_bounds__(NT) void smp_row(SmpArgs A) {
     bool dense = A.force_dense != 0;
     int64_t ncand = 0;
     bool sorted = false;
+    // a single draw that the wave path takes: its weights and scores can be
+    // computed while the candidates are ranked
+    const bool pre_draw = A.out_ids != nullptr && !P.greedy && (A.mode == MODE_VERIFY || A.n_draws == 1);
+    bool have_pre = false;
     if (!dense) {
       const uint32_t cnt = sh.count;
       if (cnt <= (uint32_t)BUFCAP) {
-        // wave 0 alone: order-free compaction of the buffer, then (<= 64
-        // survivors, the common case) a rank sort by broadcast comparisons
-        if (wave == 0) {
-          uint32_t m = 0;
-          for (uint32_t i0 = 0; i0 < cnt; i0 += 64) {
-            const uint32_t i = i0 + (uint32_t)lane;
-            const uint64_t e = i < cnt ? fl.buf[i] : 0ull;
-            const bool k = i < cnt && pk_key(e) >= theta_f;
-            const uint64_t km = __ballot(k);
-            const uint32_t slot = m + lanes_below(km);
+        // every wave: order-free compaction of the buffer (one LDS atomic
+        // per wave and pass; sh.ctr was cleared at the start) ...
+        for (uint32_t i0 = 0; i0 < cnt; i0 += NT) {
+          const uint32_t i = i0 + (uint32_t)tid;
+          const uint64_t e = i < cnt ? fl.buf[i] : 0ull;
+          const bool k = i < cnt && pk_key(e) >= theta_f;
+          const uint64_t km = __ballot(k);
+          if (km) {
+            uint32_t base = 0u;
+            if (lane == 0) base = atomicAdd(&sh.ctr, (uint32_t)__popcll(km));
+            base = (uint32_t)__builtin_amdgcn_readfirstlane((int)base);
+            const uint32_t slot = base + lanes_below(km);
             if (k && slot < (uint32_t)CAP) fl.cand[slot] = e;
-            m += (uint32_t)__popcll(km);
           }
-          if (m <= 64u) {
-            const uint64_t x = (uint32_t)lane < m ? fl.cand[lane] : 0ull;
-            uint32_t rank = 0;
-            for (uint32_t j = 0; j < m; ++j) {
-              const uint64_t y = ((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(x >> 32), (int)j) << 32) |
-                                 (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)x, (int)j);
-              rank += y > x ? 1u : 0u;
+        }
+        __syncthreads();
+        const uint32_t m = sh.ctr;
+        if (m <= 64u) {
+          // ... then (<= 64 survivors, the common case) a rank sort: thread
+          // t of waves 0..3 compares survivor t % 64 with survivors
+          // 16 (t / 64) .. +15 and adds the number above it to that
+          // survivor's rank. Meanwhile, for a single draw, wave 4 computes
+          // each survivor's weight exp_d(z) and wave 5 its version-3 score
+          // z + g (z = (l - M) / T with M the row maximum, the first sorted
+          // value), in the order the draw reads them once permuted.
+          const uint32_t i = (uint32_t)tid & 63u;
+          const uint64_t x = i < m ? fl.cand[i] : 0ull;
+          if (wave < 4) {
+            const uint32_t j0 = (uint32_t)wave * 16u;
+            if (i < m && j0 < m) {
+              uint32_t above = 0u;
+#pragma unroll
+              for (uint32_t j = 0; j < 16; ++j) above += (j0 + j < m && fl.cand[j0 + j] > x) ? 1u : 0u;
+              if (above) atomicAdd(&s_rank[i], above);
             }
-            if ((uint32_t)lane < m) fl.cand[rank] = x;
+          } else if (pre_draw && wave == 4) {
+            if (i < m) s_wpre[i] = exp_d_inline(((double)key2f(pk_key(x)) - (double)M) / P.temperature);
+          } else if (pre_draw && wave == 5 && P.version == YSKN_V3) {
+            if (i < m) {
+              const double z = ((double)key2f(pk_key(x)) - (double)M) / P.temperature;
+              s_spre[i] = z + gumbel_from_key<true>(position_key(P.seed, s_pos), pk_id(x));
+            }
           }
-          if (lane == 0) sh.ctr = m;
+          __syncthreads();
+          if ((uint32_t)tid < m) {  // wave 0 holds survivors 0..m-1
+            const uint32_t r = s_rank[tid];
+            fl.cand[r] = x;
+            if (pre_draw) {
+              fl.w[r] = s_wpre[tid];
+              fl.w[64 + r] = s_spre[tid];
+            }
+          }
+          have_pre = pre_draw;
         }
         __syncthreads();
         ncand = (int64_t)sh.ctr;
@@ -1504,6 +1556,14 @@ __global__ __launch_bounds__(NT) void smp_row(SmpArgs A) {
     // sign the key drops, and for penalised rows, whose keys are of the
     // penalised values): only those are read again from the logits.
     const int ot = tid - 64;  // wave 1's lanes: 0..63
+    // log of the mass (wave 1 alone, off the draw's path): one term per
+    // wave, in lanes 0..NW-1
+    double logZ = 0.0;
+    if (A.want_mass && wave == 1) {
+      double t = 0.0;
+      if (lane < NW && s_mref[lane] != -__builtin_inff()) t = s_mass[lane] * exp((double)s_mref[lane] - (double)M);
+      logZ = log(wave_sum_f64_dpp(t));
+    }
     auto raw_value = [&](uint64_t p) -> float {
       const float v = key2f(pk_key(p));
       if (PEN || v == 0.0f) return __uint_as_float(value_bits<DT, PEN>(rc, pk_id(p)));
@@ -1567,7 +1627,7 @@ __global__ __launch_bounds__(NT) void smp_row(SmpArgs A) {
             const int nrel = (int)__popcll(__ballot(lane < ncand && pk_key(cand[lane < ncand ? lane : 0]) >= trel));
             c = (int)plan.k_eff < nrel ? (int)plan.k_eff : nrel;
           }
-          sample_tail_wave(A, P, row, cand, c);
+          sample_tail_wave(A, P, row, cand, c, s_pos, fl.w, have_pre && !dense);
         }
       } else {
         int64_t c;

@@ -20,7 +20,7 @@ __device__ __forceinline__ double pm_hilo(uint32_t hi, uint32_t lo) {
 __device__ __forceinline__ uint64_t pm_bits(double x) { return (uint64_t)__double_as_longlong(x); }
 
 // exp(value) in binary64; portable_math.rs:224-283.
-__device__ __noinline__ double exp_d(double value) {
+__device__ __forceinline__ double exp_d_inline(double value) {
   const uint64_t b = pm_bits(value);
   const uint32_t hi = (uint32_t)(b >> 32), lo = (uint32_t)b;
   const bool neg = (hi >> 31) != 0;
@@ -82,7 +82,7 @@ __device__ __noinline__ double exp_d(double value) {
 }
 
 // log(value) in binary64 without a zero special case; portable_math.rs:297-364.
-__device__ __noinline__ double log_d(double value) {
+__device__ __forceinline__ double log_d_inline(double value) {
   int32_t hx = (int32_t)(uint32_t)(pm_bits(value) >> 32);
   int32_t k = 0;
   if (hx < 0x00100000) {
@@ -158,6 +158,11 @@ __device__ __noinline__ double log_d(double value) {
   return a - u;
 }
 
+// Out-of-line copies for the block-wide paths (code size); the per-wave
+// draw inlines the bodies above.
+__device__ __noinline__ double exp_d(double value) { return exp_d_inline(value); }
+__device__ __noinline__ double log_d(double value) { return log_d_inline(value); }
+
 // SplitMix64 finaliser; output_head_sampler.rs:214-219.
 __host__ __device__ __forceinline__ uint64_t mix64(uint64_t z) {
   z += 0x9e3779b97f4a7c15ull;
@@ -168,10 +173,12 @@ __host__ __device__ __forceinline__ uint64_t mix64(uint64_t z) {
 
 // Token-keyed Gumbel noise given the per-(seed, position) hash
 // b = mix64(mix64(seed) ^ position); output_head_sampler.rs:221-228.
+template <bool INLINE = false>
 __device__ __forceinline__ double gumbel_from_key(uint64_t b, uint32_t token) {
   const uint64_t h = mix64(b ^ ((uint64_t)token * 0xd6e8feb86659fd93ull));
   double u = (double)(h >> 11) + 0.5;
   u = u * (1.0 / 9007199254740992.0);
+  if (INLINE) return -log_d_inline(-log_d_inline(u));
   return -log_d(-log_d(u));
 }
 
