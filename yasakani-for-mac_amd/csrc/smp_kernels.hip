@@ -939,13 +939,14 @@ __device__ __forceinline__ void load_chunk(const RowCtx& rc, int32_t V, int nch,
   }
 }
 
-// Raw bits of full chunk c through 16-byte buffer loads, no guards: the
-// caller ensures the chunk lies inside the row and the row is 16-byte
-// aligned. The loads take a uniform chunk offset in an SGPR and
-// loop-invariant lane offsets in VGPRs, so the stream spends no vector
-// instructions on addresses. With `live` false the same loads go through a
-// resource of size 0: every one is out of range, returns zeros and touches
-// no memory. Issuing the same loads on every path, and keeping address
+// Raw bits of chunk c through 16-byte buffer loads, no guards: the caller
+// ensures the row is 16-byte aligned (so its length is a multiple of the
+// 16-byte groups). The resource spans exactly the row: groups of the last,
+// ragged chunk past its end are out of range and return zeros without
+// touching memory (chunk_values ignores them). The loads take a uniform
+// chunk offset in an SGPR and loop-invariant lane offsets in VGPRs, so the
+// stream spends no vector instructions on addresses. With `live` false the
+// same loads go through a resource of size 0: every one is out of range. Issuing the same loads on every path, and keeping address
 // arithmetic out of the destination registers, lets the compiler wait for
 // exactly the buffer it is about to read, with the other still in flight.
 template <int DT>
@@ -1045,6 +1046,7 @@ struct RowShared {
   uint32_t bw[BW_N];   // shared bounds (BW_*)
   uint32_t ndef;       // deferred chunks recorded (may exceed DEFCAP: those were not deferred)
   uint32_t ctr;        // compaction counter
+  uint32_t next;       // next chunk of the stream not yet claimed by a wave
 };
 
 // Mass terms (if mass) and candidates of chunk c for threshold thr. Work is
@@ -1063,7 +1065,7 @@ struct RowShared {
 // end, and only if that key reaches the final bound.
 template <int DT>
 __device__ __forceinline__ void chunk_filter(int c, int lane, const uint32_t (&kb)[EPT], uint32_t thr,
-                                             uint32_t mk, bool mass, uint32_t cmax, int defer_lanes,
+                                             uint32_t mk, bool mass, uint32_t lk, uint32_t cmax, int defer_lanes,
                                              WaveState& ws, RowShared& sh, RowLds& fl, uint64_t* spill) {
   constexpr int GRP = (DT == 0) ? 4 : 8;
   constexpr int NGRP = EPT / GRP;
@@ -1080,7 +1082,10 @@ __device__ __forceinline__ void chunk_filter(int c, int lane, const uint32_t (&k
   }
   float tany = fminf(thf, lo);
   // nothing in the chunk reaches the lower of the two cuts: no work at all
-  if (!(key2f(cmax) >= tany)) return;
+  // (lk: this lane's largest key, 0 for none; cmax: the chunk's, 0 if not
+  // known yet)
+  const float lkf = lk == 0u ? -__builtin_inff() : key2f(lk);
+  if (!__ballot(lkf >= tany)) return;
   float gmax[NGRP];
   float lmax = -__builtin_inff();
 #pragma unroll
@@ -1097,6 +1102,7 @@ __device__ __forceinline__ void chunk_filter(int c, int lane, const uint32_t (&k
     if (lane == 0) idx = atomicAdd(&sh.ndef, 1u);
     idx = (uint32_t)__builtin_amdgcn_readfirstlane((int)idx);
     if (idx < (uint32_t)DEFCAP) {
+      if (cmax == 0u) cmax = wave_max_dpp(lk);
       if (lane == 0) fl.def[idx] = make_uint2((uint32_t)c, cmax);
       keep_any = false;
       tany = lo;
@@ -1225,6 +1231,7 @@ __global__ __launch_bounds__(NT) void smp_row(SmpArgs A) {
     sh.count = 0u;
     sh.flags = 0u;
     sh.ndef = 0u;
+    sh.next = 2u * NW;  // chunks 0 .. 2 NW - 1 are the waves' first two
   }
   if (tid < BW_N) sh.bw[tid] = 0u;
   if (tid < 64) s_rank[tid] = 0u;
@@ -1236,10 +1243,11 @@ __global__ __launch_bounds__(NT) void smp_row(SmpArgs A) {
   ws.m_ref = -__builtin_inff();
   ws.acc = 0.0;
   ws.bad = false;
-  // Chunks [0, nfull) are read by the double-buffered stream with unguarded
-  // 16-byte loads; the rest (the ragged last chunk of an aligned row, every
-  // chunk of an unaligned one) through the guarded path after it.
-  const int nfull = VEC ? V / WSEG : 0;
+  // Chunks [0, nfull) are read by the double-buffered stream with
+  // range-checked buffer loads: every chunk of an aligned row, the ragged
+  // last one included. An unaligned row goes through the guarded path after
+  // it instead.
+  const int nfull = VEC ? nch : 0;
   uint32_t buf0[EPT], buf1[EPT];
   load_full<DT>(rc.base, V, wave, wave < nfull, lane, buf0);
   __builtin_amdgcn_sched_barrier(0);  // buf0's loads first: the stream waits for them first
@@ -1272,30 +1280,40 @@ __global__ __launch_bounds__(NT) void smp_row(SmpArgs A) {
   // one comparison; the bounds only rise, so a stale lo_f is merely low.
   float lo_f = -__builtin_inff();
 
-  // one chunk: c from X; in the stream, prefetch the wave's chunk two steps
-  // ahead into X
-  auto step = [&](uint32_t (&X)[EPT], int c, bool first, bool stream) {
+  // One chunk: c from X. In the stream, the wave claims its next chunk and
+  // prefetches it into X (the claim is an LDS atomic issued first, its
+  // result read last, so that its latency is hidden); returns that chunk.
+  auto step = [&](uint32_t (&X)[EPT], int c, bool first, bool stream) -> int {
+    uint32_t ticket = 0u;
+    if (stream && lane == 0) ticket = atomicAdd(&sh.next, 1u);
     float lmax = -__builtin_inff();
-    chunk_values<DT, PEN>(rc, V, c, lane, X, lmax, ws.bad);
-    if (first || __ballot(lmax >= lo_f)) {
-      uint32_t lk = lmax == -__builtin_inff() ? 0u : f2key(__float_as_uint(lmax));
+    const bool live = c < nch;
+    if (live) chunk_values<DT, PEN>(rc, V, c, lane, X, lmax, ws.bad);
+    if (live && (first || __ballot(lmax >= lo_f))) {
+      const uint32_t lk = lmax == -__builtin_inff() ? 0u : f2key(__float_as_uint(lmax));
+      // The chunk maximum (a DPP reduction) only when a lane maximum may
+      // enter the list or raise the wave's maximum.
       uint32_t cmax = 0u;
-      const int rr = first ? r_first : r_next;
-      for (int i = 0; i < rr; ++i) {
-        const uint32_t m = wave_max_dpp(lk);
-        if (i == 0) cmax = m;
-        if (m <= theta_w || m <= th_row) break;  // 0, cannot enter the full list, or below the row bound
-        // insert m: entries >= m keep their lanes, the rest move up by one
-        const uint32_t pos = (uint32_t)__popcll(__ballot(lane < plan.KB && lst >= m));
-        const uint32_t up = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)lst, 0x138, 0xf, 0xf, false);  // wave_shr:1
-        lst = (uint32_t)lane < pos ? lst : ((uint32_t)lane == pos ? m : up);
-        theta_w = (uint32_t)__builtin_amdgcn_readlane((int)lst, plan.KB - 1);
-        const uint64_t eq = __ballot(lk == m);
-        if (lane == (int)__builtin_ctzll(eq)) lk = 0u;
-      }
-      if (cmax > ws.wkey) {
-        ws.wkey = cmax;
-        if (lane == 0) atomicMax(&sh.bw[BW_MKEY], cmax);
+      const uint32_t lb = theta_w > th_row ? theta_w : th_row;
+      if (first || __ballot(lk > lb || lk > ws.wkey)) {
+        uint32_t rk = lk;
+        const int rr = first ? r_first : r_next;
+        for (int i = 0; i < rr; ++i) {
+          const uint32_t m = wave_max_dpp(rk);
+          if (i == 0) cmax = m;
+          if (m <= theta_w || m <= th_row) break;  // 0, cannot enter the full list, or below the row bound
+          // insert m: entries >= m keep their lanes, the rest move up by one
+          const uint32_t pos = (uint32_t)__popcll(__ballot(lane < plan.KB && lst >= m));
+          const uint32_t up = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)lst, 0x138, 0xf, 0xf, false);  // wave_shr:1
+          lst = (uint32_t)lane < pos ? lst : ((uint32_t)lane == pos ? m : up);
+          theta_w = (uint32_t)__builtin_amdgcn_readlane((int)lst, plan.KB - 1);
+          const uint64_t eq = __ballot(rk == m);
+          if (lane == (int)__builtin_ctzll(eq)) rk = 0u;
+        }
+        if (cmax > ws.wkey) {
+          ws.wkey = cmax;
+          if (lane == 0) atomicMax(&sh.bw[BW_MKEY], cmax);
+        }
       }
       if (theta_w > theta_pub) {
         // every bound a wave uses must reach the shared one: the final
@@ -1346,34 +1364,50 @@ __global__ __launch_bounds__(NT) void smp_row(SmpArgs A) {
       // (a wave's first chunk has about KB lanes with survivors by
       // construction -- the lane maxima that set its first bound -- so its
       // deferral limit is raised by KB)
-      chunk_filter<DT>(c, lane, X, thr, mk, A.want_mass != 0, cmax, first ? DLANES + plan.KB : DLANES, ws, sh,
-                       fl, spill);
+      chunk_filter<DT>(c, lane, X, thr, mk, A.want_mass != 0, lk, cmax, first ? DLANES + plan.KB : DLANES, ws,
+                       sh, fl, spill);
       th_row = th;
       const float lo_list = key_threshold_float(theta_w > th ? theta_w : th);
       const float lo_cand = key_threshold_float(thr);
       const float lo_mass = A.want_mass ? ws.m_ref - ZMASS : __builtin_inff();
       lo_f = mk == 0u ? -__builtin_inff() : fminf(fminf(lo_list, lo_cand), lo_mass);
     }
-    if (stream) load_full<DT>(rc.base, V, c + 2 * NW, c + 2 * NW < nfull, lane, X);
+    int nx = nfull;
+    if (stream) {
+      nx = __builtin_amdgcn_readfirstlane((int)ticket);
+      load_full<DT>(rc.base, V, nx, nx < nfull, lane, X);
+    }
+    return nx;
   };
-  // pairs of steps with no condition between them: at every step the buffer
-  // read is the older of the two in flight, on entry and around the loop
-  const int nmine = wave < nfull ? (nfull - wave + NW - 1) / NW : 0;
-  int c = wave;
-  for (int i = 0; i + 1 < nmine; i += 2, c += 2 * NW) {
-    step(buf0, c, i == 0, true);
-    step(buf1, c + NW, false, true);
+  // The first draw's position: a global load waits behind the other rows'
+  // streams (microseconds), so it is read now, at the start, by the last
+  // wave; the chunks it meanwhile leaves go to the other waves.
+  // (a uniform branch: a scalar load, which leaves the vector-memory
+  // counter, and so the stream's waits, alone)
+  if (wave == NW - 1 && A.out_ids != nullptr) {
+    const uint64_t p0 = position_of(A, row, 0);
+    if (lane == 0) s_pos = p0;
   }
-  if (nmine & 1) step(buf0, c, nmine == 1, true);
+  // Chunks [0, nfull) are handed out as the waves free their buffers: wave w
+  // starts with chunks w and w + NW (already requested) and then claims the
+  // next unclaimed chunk, so that a wave slowed by heavy chunks takes fewer
+  // of them. At every step the buffer read is the older of the two in
+  // flight; a claim past nfull ends the wave's stream (claims only grow, so
+  // the other buffer's chunk, claimed earlier, was the smaller).
+  {
+    int c0 = wave, c1 = wave + NW;
+    bool first = true;
+    while (c0 < nfull) {
+      c0 = step(buf0, c0, first, true);
+      first = false;
+      c1 = step(buf1, c1, false, true);  // (c1 may be past the end: then nothing but the claim)
+    }
+  }
   // the remaining chunks, each by the wave the round-robin order gives it
-  for (c = nfull + (wave - nfull % NW + NW) % NW; c < nch; c += NW) {
+  for (int c = nfull + (wave - nfull % NW + NW) % NW; c < nch; c += NW) {
     load_chunk<DT, VEC>(rc, V, nch, c, lane, buf0);
     step(buf0, c, c == wave, false);
   }
-  // The first draw's position: a global load waits behind the other rows'
-  // streams (microseconds), so it is read here, by the last wave, which
-  // has the fewest chunks and would wait at the barrier below anyway.
-  if (tid == (NW - 1) * 64 && A.out_ids != nullptr) s_pos = position_of(A, row, 0);
   // A final bound from the union of the waves' lists: the KB-th largest of
   // their top 8 entries (64 distinct elements). It is at least the minimum
   // over the waves of their ceil(KB/8)-th values, and sh.bw[BW_THETA] keeps
@@ -1420,7 +1454,8 @@ __global__ __launch_bounds__(NT) void smp_row(SmpArgs A) {
         float lmax = -__builtin_inff();
         bool bad = false;
         chunk_values<DT, PEN>(rc, V, cc, lane, X, lmax, bad);
-        chunk_filter<DT>(cc, lane, X, thr_f, mkf, false, fl.def[i].y, 64, ws, sh, fl, spill);
+        const uint32_t lkr = lmax == -__builtin_inff() ? 0u : f2key(__float_as_uint(lmax));
+        chunk_filter<DT>(cc, lane, X, thr_f, mkf, false, lkr, fl.def[i].y, 64, ws, sh, fl, spill);
       };
       uint32_t ia = next((uint32_t)wave);
       uint32_t ib = ia < nd ? next(ia + NW) : nd;
