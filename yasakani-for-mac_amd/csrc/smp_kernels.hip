@@ -1023,13 +1023,44 @@ __device__ __forceinline__ void chunk_values(const RowCtx& rc, int32_t V, int c,
   }
 }
 
+// Appended candidates go to per-wave blocks of ABLK slots of the append
+// buffer (slots past BUFCAP are in the row's spill area): a wave reserves a
+// block with one LDS atomic and fills it in order, so the common append
+// costs no atomic. Slots a wave leaves unused are cleared to 0 (key 0 is
+// below every threshold).
+constexpr uint32_t ABLK = 64;
+
 // Per-wave streaming state.
 struct WaveState {
-  uint32_t wkey;  // largest key this wave has seen (uniform)
-  float m_ref;    // reference point of the wave's logprob mass (uniform)
-  double acc;     // per lane: sum of exp(l - m_ref) over l >= m_ref - ZMASS
-  bool bad;       // per lane: a non-finite value was seen
+  uint32_t wkey;    // largest key this wave has seen (uniform)
+  float m_ref;      // reference point of the wave's logprob mass (uniform)
+  double acc;       // per lane: sum of exp(l - m_ref) over l >= m_ref - ZMASS
+  bool bad;         // per lane: a non-finite value was seen
+  uint32_t ab_cur;  // next free slot of the wave's append block (uniform)
+  uint32_t ab_end;  // end of that block
+  uint32_t spill_cap;  // slots of the row's spill area
 };
+
+// Entry e (per lane, where k) to slot `slot` of the append buffer or, past
+// BUFCAP, of the spill area (reservations past the spill area are dropped:
+// the finish then takes the dense path).
+__device__ __forceinline__ void put_entry(RowLds& fl, uint64_t* spill, uint32_t spill_cap, uint32_t slot,
+                                          uint64_t e, bool k, bool& spilled) {
+  if (k && slot < (uint32_t)BUFCAP) ((lds_u64*)fl.buf)[slot] = e;
+  if (k && slot >= (uint32_t)BUFCAP && slot - (uint32_t)BUFCAP < spill_cap) {
+    __builtin_nontemporal_store(e, &((global_u64*)spill)[slot - BUFCAP]);
+    spilled = true;
+  }
+}
+
+// Clears the rest of the wave's append block.
+__device__ __forceinline__ void close_block(WaveState& ws, RowLds& fl, uint64_t* spill, int lane, bool& spilled) {
+  for (uint32_t s0 = ws.ab_cur; s0 < ws.ab_end; s0 += 64) {
+    const uint32_t slot = s0 + (uint32_t)lane;
+    put_entry(fl, spill, ws.spill_cap, slot, 0ull, slot < ws.ab_end, spilled);
+  }
+  ws.ab_cur = ws.ab_end;
+}
 
 // Shared streaming state of a row block.
 // The bounds the waves share sit in one array so that a wave reads all of
@@ -1110,8 +1141,7 @@ __device__ __forceinline__ void chunk_filter(int c, int lane, const uint32_t (&k
     }
   }
   const uint32_t eb = (uint32_t)c * WSEG + (uint32_t)lane * GRP;
-  // pass 1: mass terms, and the number of candidates of the chunk
-  uint32_t nk = 0u;
+  bool spilled = false;
 #pragma unroll
   for (int q = 0; q < NGRP; ++q) {
     if (!__ballot(gmax[q] >= tany)) continue;
@@ -1120,40 +1150,29 @@ __device__ __forceinline__ void chunk_filter(int c, int lane, const uint32_t (&k
       const float v = __uint_as_float(kb[q * GRP + j]);
       if (!__ballot(v >= tany)) continue;
       if (v >= lo) ws.acc += (double)__builtin_amdgcn_exp2f((v - ws.m_ref) * 1.4426950408889634f);
-      if (keep_any) nk += (uint32_t)__popcll(__ballot(v >= thf));
-    }
-  }
-  if (nk == 0u) return;
-  // pass 2: one LDS atomic reserves the chunk's slots; the candidates are
-  // written in (group, element, lane) order
-  uint32_t base = 0u;
-  if (lane == 0) base = atomicAdd(&sh.count, nk);
-  base = (uint32_t)__builtin_amdgcn_readfirstlane((int)base);
-  const bool fits = base + nk <= (uint32_t)BUFCAP;
-  bool spilled = false;
-#pragma unroll
-  for (int q = 0; q < NGRP; ++q) {
-    if (!__ballot(gmax[q] >= thf)) continue;
-#pragma unroll
-    for (int j = 0; j < GRP; ++j) {
-      const float v = __uint_as_float(kb[q * GRP + j]);
-      const bool k = v >= thf;
-      const uint64_t km = __ballot(k);
-      if (!km) continue;
-      const uint32_t slot = base + lanes_below(km);
-      const uint64_t e = pack(f2key(__float_as_uint(v)), eb + (uint32_t)(q * 64 * GRP + j));
-      if (fits) {
-        if (k) ((lds_u64*)fl.buf)[slot] = e;
-      } else {
-        // rare: the buffer is full; below BUFCAP to LDS, the rest to the
-        // spill area
-        if (k && slot < (uint32_t)BUFCAP) ((lds_u64*)fl.buf)[slot] = e;
-        if (k && slot >= (uint32_t)BUFCAP) __builtin_nontemporal_store(e, &((global_u64*)spill)[slot - BUFCAP]);
-        spilled = true;
+      if (keep_any) {
+        const bool k = v >= thf;
+        const uint64_t km = __ballot(k);
+        if (km) {
+          const uint32_t n = (uint32_t)__popcll(km);
+          if (ws.ab_cur + n > ws.ab_end) {
+            // the block is full: clear its rest, reserve the next
+            close_block(ws, fl, spill, lane, spilled);
+            uint32_t base = 0u;
+            if (lane == 0) base = atomicAdd(&sh.count, ABLK);
+            base = (uint32_t)__builtin_amdgcn_readfirstlane((int)base);
+            ws.ab_cur = base;
+            ws.ab_end = base + ABLK;
+          }
+          const uint64_t e = pack(f2key(__float_as_uint(v)), eb + (uint32_t)(q * 64 * GRP + j));
+          put_entry(fl, spill, ws.spill_cap, ws.ab_cur + lanes_below(km), e, k, spilled);
+          ws.ab_cur += n;
+        }
       }
-      base += (uint32_t)__popcll(km);
     }
   }
+  // the rare spill stores end with a full wait, so the common path holds
+  // only LDS stores and the compiler keeps the prefetched chunk in flight
   if (spilled) __builtin_amdgcn_s_waitcnt(0);
 }
 
@@ -1243,6 +1262,9 @@ __global__ __launch_bounds__(NT) void smp_row(SmpArgs A) {
   ws.m_ref = -__builtin_inff();
   ws.acc = 0.0;
   ws.bad = false;
+  ws.ab_cur = 0u;
+  ws.ab_end = 0u;
+  ws.spill_cap = (uint32_t)A.dense_ld;
   // Chunks [0, nfull) are read by the double-buffered stream with
   // range-checked buffer loads: every chunk of an aligned row, the ragged
   // last one included. An unaligned row goes through the guarded path after
@@ -1415,6 +1437,11 @@ __global__ __launch_bounds__(NT) void smp_row(SmpArgs A) {
   // final one (every improvement was published), which keeps the buffer
   // complete down to it.
   if (lane < 8) fl.lists[wave * 8 + lane] = lane < plan.KB ? lst : 0u;
+  {
+    bool sp = false;
+    close_block(ws, fl, spill, lane, sp);
+    if (sp) __builtin_amdgcn_s_waitcnt(0);
+  }
   // The wave's own results, which the deferred reads below do not change
   // (they add no mass terms and find no new maximum).
   if (__ballot(ws.bad)) wflags |= F_NONFINITE;
@@ -1471,6 +1498,11 @@ __global__ __launch_bounds__(NT) void smp_row(SmpArgs A) {
         if (id < nd) load_chunk<DT, VEC>(rc, V, nch, (int)fl.def[id].x, lane, buf1);
         ia = ic;
         ib = id;
+      }
+      {
+        bool sp = false;
+        close_block(ws, fl, spill, lane, sp);
+        if (sp) __builtin_amdgcn_s_waitcnt(0);
       }
       __syncthreads();  // the deferred chunks' appends are in LDS
     }
@@ -1556,10 +1588,12 @@ __global__ __launch_bounds__(NT) void smp_row(SmpArgs A) {
         __syncthreads();
         ncand = (int64_t)sh.ctr;
         sorted = ncand <= 64;
-      } else {
+      } else if (cnt - (uint32_t)BUFCAP <= (uint32_t)A.dense_ld) {
         uint32_t nc = compact_entries(fl.buf, BUFCAP, fl.cand, CAP, theta_f, &sh.ctr, true);
         nc = compact_entries(spill, cnt - (uint32_t)BUFCAP, fl.cand, CAP, theta_f, &sh.ctr, false);
         ncand = (int64_t)nc;
+      } else {
+        ncand = (int64_t)CAP + 1;  // reservations outran the spill area: the dense path
       }
       dense = ncand > CAP || ncand < 1;
     }
