@@ -39,6 +39,8 @@ constexpr int32_t YSKN_V3 = 3;
 // memory and the LDS counters, so every wait after it becomes a full wait.
 typedef __attribute__((address_space(3))) uint64_t lds_u64;
 typedef __attribute__((address_space(1))) uint64_t global_u64;
+typedef __attribute__((ext_vector_type(4))) uint32_t u32x4;
+typedef __attribute__((address_space(3))) u32x4 lds_u4;
 
 // ---------------------------------------------------------------------------
 // keys and packing
@@ -1030,6 +1032,35 @@ __device__ __forceinline__ void chunk_values(const RowCtx& rc, int32_t V, int c,
 // below every threshold).
 constexpr uint32_t ABLK = 64;
 
+// The first NSTASH deferred chunks keep their converted values in LDS, in
+// the candidate and weight arrays (unused until the finish): their second
+// pass reads LDS instead of memory. Slot s holds lane l's values
+// 4q .. 4q + 3 at uint4 s * 512 + q * 64 + l.
+constexpr uint32_t NSTASH = (CAP * 16) / (WSEG * 4);
+__device__ __forceinline__ void stash_chunk(RowLds& fl, uint32_t s, int lane, const uint32_t (&kb)[EPT]) {
+  lds_u4* S = (lds_u4*)fl.cand + s * 512u + (uint32_t)lane;
+#pragma unroll
+  for (int q = 0; q < EPT / 4; ++q) {
+    u32x4 v;
+    v.x = kb[4 * q];
+    v.y = kb[4 * q + 1];
+    v.z = kb[4 * q + 2];
+    v.w = kb[4 * q + 3];
+    S[q * 64] = v;
+  }
+}
+__device__ __forceinline__ void unstash_chunk(RowLds& fl, uint32_t s, int lane, uint32_t (&kb)[EPT]) {
+  const lds_u4* S = (const lds_u4*)fl.cand + s * 512u + (uint32_t)lane;
+#pragma unroll
+  for (int q = 0; q < EPT / 4; ++q) {
+    const u32x4 v = S[q * 64];
+    kb[4 * q] = v.x;
+    kb[4 * q + 1] = v.y;
+    kb[4 * q + 2] = v.z;
+    kb[4 * q + 3] = v.w;
+  }
+}
+
 // Per-wave streaming state.
 struct WaveState {
   uint32_t wkey;    // largest key this wave has seen (uniform)
@@ -1134,7 +1165,13 @@ __device__ __forceinline__ void chunk_filter(int c, int lane, const uint32_t (&k
     idx = (uint32_t)__builtin_amdgcn_readfirstlane((int)idx);
     if (idx < (uint32_t)DEFCAP) {
       if (cmax == 0u) cmax = wave_max_dpp(lk);
-      if (lane == 0) fl.def[idx] = make_uint2((uint32_t)c, cmax);
+      // (chunk, stash slot + 1 or 0) in the record's first word
+      uint32_t code = (uint32_t)c;
+      if (idx < NSTASH) {
+        stash_chunk(fl, idx, lane, kb);
+        code |= (idx + 1u) << 16;
+      }
+      if (lane == 0) fl.def[idx] = make_uint2(code, cmax);
       keep_any = false;
       tany = lo;
       if (!(key2f(cmax) >= tany)) return;
@@ -1476,26 +1513,39 @@ __global__ __launch_bounds__(NT) void smp_row(SmpArgs A) {
           if (fl.def[i].y >= thr_f) return i;
         return nd;
       };
+      // a stashed chunk comes from LDS, converted already; the others from
+      // memory again
+      auto fetch = [&](uint32_t (&X)[EPT], uint32_t i) {
+        const uint32_t code = fl.def[i].x;
+        if ((code >> 16) == 0u) load_chunk<DT, VEC>(rc, V, nch, (int)(code & 0xffffu), lane, X);
+      };
       auto redo = [&](uint32_t (&X)[EPT], uint32_t i) {
-        const int cc = (int)fl.def[i].x;
+        const uint32_t code = fl.def[i].x;
+        const int cc = (int)(code & 0xffffu);
         float lmax = -__builtin_inff();
-        bool bad = false;
-        chunk_values<DT, PEN>(rc, V, cc, lane, X, lmax, bad);
+        if ((code >> 16) != 0u) {
+          unstash_chunk(fl, (code >> 16) - 1u, lane, X);
+#pragma unroll
+          for (int k = 0; k < EPT; ++k) lmax = fmaxf(lmax, __uint_as_float(X[k]));
+        } else {
+          bool bad = false;
+          chunk_values<DT, PEN>(rc, V, cc, lane, X, lmax, bad);
+        }
         const uint32_t lkr = lmax == -__builtin_inff() ? 0u : f2key(__float_as_uint(lmax));
         chunk_filter<DT>(cc, lane, X, thr_f, mkf, false, lkr, fl.def[i].y, 64, ws, sh, fl, spill);
       };
       uint32_t ia = next((uint32_t)wave);
       uint32_t ib = ia < nd ? next(ia + NW) : nd;
-      if (ia < nd) load_chunk<DT, VEC>(rc, V, nch, (int)fl.def[ia].x, lane, buf0);
-      if (ib < nd) load_chunk<DT, VEC>(rc, V, nch, (int)fl.def[ib].x, lane, buf1);
+      if (ia < nd) fetch(buf0, ia);
+      if (ib < nd) fetch(buf1, ib);
       while (ia < nd) {
         redo(buf0, ia);
         const uint32_t ic = ib < nd ? next(ib + NW) : nd;
-        if (ic < nd) load_chunk<DT, VEC>(rc, V, nch, (int)fl.def[ic].x, lane, buf0);
+        if (ic < nd) fetch(buf0, ic);
         if (ib >= nd) break;
         redo(buf1, ib);
         const uint32_t id = ic < nd ? next(ic + NW) : nd;
-        if (id < nd) load_chunk<DT, VEC>(rc, V, nch, (int)fl.def[id].x, lane, buf1);
+        if (id < nd) fetch(buf1, id);
         ia = ic;
         ib = id;
       }
