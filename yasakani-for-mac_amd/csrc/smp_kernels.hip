@@ -530,11 +530,12 @@ __device__ __forceinline__ double lane_f64(double x, int j) {
   return __longlong_as_double((long long)(((uint64_t)hi << 32) | lo));
 }
 
-// With `have_pre`, pre[j] and pre[64 + j] already hold candidate j's weight
-// and (version 3) score, computed by other waves while the candidates were
-// being ranked.
+// pre: LDS scratch of at least 128 binary64 values. With `have_pre`, pre[j]
+// and pre[64 + j] already hold candidate j's weight and (version 3) score,
+// computed by other waves while the candidates were being ranked; otherwise
+// the weights are computed here and written to pre[j].
 __device__ __forceinline__ void sample_tail_wave(const SmpArgs& A, const DevParams& P, int row,
-                                                 const uint64_t* cand, int c, uint64_t pos, const double* pre,
+                                                 const uint64_t* cand, int c, uint64_t pos, double* pre,
                                                  bool have_pre) {
   const int lane = threadIdx.x & 63;
   const double T = P.temperature;
@@ -554,10 +555,21 @@ __device__ __forceinline__ void sample_tail_wave(const SmpArgs& A, const DevPara
   }
   // The serial binary64 prefix sums in candidate order, one pass: lane j
   // keeps prefix_j = (..((w_0 + w_1) + w_2) ..) + w_j; the total is the last.
+  // The weights are read from LDS by every lane at once (broadcast reads,
+  // eight issued ahead of their adds), so the chain is the adds alone.
+  if (!have_pre && in) pre[lane] = w;  // (the wave's own LDS writes precede its reads)
   double prefix = 0.0, pre_j = 0.0;
-  for (int j = 0; j < c; ++j) {
-    prefix = prefix + lane_f64(w, j);
-    pre_j = lane == j ? prefix : pre_j;
+  for (int j0 = 0; j0 < c; j0 += 8) {
+    double v[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) v[k] = pre[j0 + k];  // (c <= 64 < CAP: in bounds)
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      if (j0 + k < c) {
+        prefix = prefix + v[k];
+        pre_j = lane == j0 + k ? prefix : pre_j;
+      }
+    }
   }
   // top-p: the first n with prefix_{n-1} >= top_p * total
   const double thr = P.top_p * prefix;
