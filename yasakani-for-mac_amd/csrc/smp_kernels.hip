@@ -1263,13 +1263,14 @@ __device__ __forceinline__ uint32_t compact_entries(const uint64_t* src, uint32_
 // ---------------------------------------------------------------------------
 // smp_row: one block of 8 wave64s per row, streaming the whole row.
 //
-// The row is read in rounds: in round k wave w takes chunk 8k + w (2,048
-// logits, 32 values per lane, coalesced 16-byte loads), with the chunk of
-// round k + 1 already in flight. One barrier per round publishes the waves'
-// maxima; every wave then filters its chunk with the row's bounds as they
-// stand and appends the elements that can matter to an LDS buffer. After the
-// last round the same block sorts the candidates and runs the reference's
-// truncation and draw: no second launch, no traffic between blocks.
+// The row is read in chunks of 2,048 logits (32 values per lane, 16-byte
+// buffer loads), two per wave in flight; the waves claim chunks as they
+// free their buffers and share bounds and the row maximum through LDS
+// atomics, with no barrier in the stream. Each wave filters its chunks with
+// the bounds as they stand and appends the elements that can matter to an
+// LDS buffer. After the stream the same block sorts the candidates and runs
+// the reference's truncation and draw: no second launch, no traffic between
+// blocks.
 // ---------------------------------------------------------------------------
 template <int DT, bool VEC, bool PEN>
 __global__ __launch_bounds__(NT) void smp_row(SmpArgs A) {
@@ -1290,11 +1291,25 @@ __global__ __launch_bounds__(NT) void smp_row(SmpArgs A) {
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int row = blockIdx.x;
   const int32_t V = A.V;
+  // The wave's first two chunks are requested before anything else: they
+  // need only the row's address, while the parameters take dependent scalar
+  // loads (microseconds at the start of a launch).
+  const char* const row_base = (const char*)A.logits + (int64_t)row * A.ld * (DT == 0 ? 4 : 2);
+  const int nch = (V + WSEG - 1) / WSEG;
+  // Chunks [0, nfull) are read by the double-buffered stream with
+  // range-checked buffer loads: every chunk of an aligned row, the ragged
+  // last one included. An unaligned row goes through the guarded path after
+  // it instead.
+  const int nfull = VEC ? nch : 0;
+  uint32_t buf0[EPT], buf1[EPT];
+  load_full<DT>(row_base, V, wave, wave < nfull, lane, buf0);
+  __builtin_amdgcn_sched_barrier(0);  // buf0's loads first: the stream waits for them first
+  load_full<DT>(row_base, V, wave + NW, wave + NW < nfull, lane, buf1);
+  __builtin_amdgcn_sched_barrier(0);  // both chunks in flight before any other work
   const DevParams P = A.prm[A.prm_shared ? 0 : row];
   const RowPlan plan = make_plan(A, P);
   uint32_t wflags = 0;
   const RowCtx rc = make_rowctx<PEN>(A, P, row, DT == 0 ? 4 : 2, &wflags);
-  const int nch = (V + WSEG - 1) / WSEG;
   if (tid == 0) {
     sh.count = 0u;
     sh.flags = 0u;
@@ -1314,16 +1329,6 @@ __global__ __launch_bounds__(NT) void smp_row(SmpArgs A) {
   ws.ab_cur = 0u;
   ws.ab_end = 0u;
   ws.spill_cap = (uint32_t)A.dense_ld;
-  // Chunks [0, nfull) are read by the double-buffered stream with
-  // range-checked buffer loads: every chunk of an aligned row, the ragged
-  // last one included. An unaligned row goes through the guarded path after
-  // it instead.
-  const int nfull = VEC ? nch : 0;
-  uint32_t buf0[EPT], buf1[EPT];
-  load_full<DT>(rc.base, V, wave, wave < nfull, lane, buf0);
-  __builtin_amdgcn_sched_barrier(0);  // buf0's loads first: the stream waits for them first
-  load_full<DT>(rc.base, V, wave + NW, wave + NW < nfull, lane, buf1);
-  __builtin_amdgcn_sched_barrier(0);  // both chunks in flight before any work
   __syncthreads();  // shared state initialised
 
   // Each wave keeps the KB largest lane maxima of its chunks so far, sorted
