@@ -1344,10 +1344,14 @@ __global__ __launch_bounds__(NT) void smp_row(SmpArgs A) {
   uint32_t thr_mk = 0u, thr_th = 0u, thr_c = 1u;  // the last row threshold and its inputs
   uint32_t theta_pub = 0u;                          // theta_w as last published
   const int qidx = (plan.KB + NW - 1) / NW - 1;
-  // per chunk: its r largest lane maxima enter the list (the first chunk: up
-  // to KB of them, so the bound exists from the start)
-  const int r_first = plan.KB < 64 ? plan.KB : 64;
-  const int r_next = plan.KB < 8 ? plan.KB : 8;
+  // per chunk: up to its two largest lane maxima enter the list. Each entry
+  // costs a wave-wide reduction on the stream's critical path (the waves'
+  // first chunks at the start most of all); the bound the list then lacks
+  // early is covered by the waves' shared third entries and the final union
+  // of their lists (measured: filling the first KB = 20 at once cost about
+  // 4 us per launch, eight per later chunk about 0.5 us).
+  const int r_first = plan.KB < 2 ? plan.KB : 2;
+  const int r_next = r_first;
 
   // Below lo_f nothing can matter to this wave: no lane maximum would enter
   // its list (lo_f <= its KB-th value), no value would be a candidate
