@@ -1346,10 +1346,12 @@ __global__ __launch_bounds__(NT) void smp_row(SmpArgs A) {
   const int qidx = (plan.KB + NW - 1) / NW - 1;
   // per chunk: up to its two largest lane maxima enter the list. Each entry
   // costs a wave-wide reduction on the stream's critical path (the waves'
-  // first chunks at the start most of all); the bound the list then lacks
-  // early is covered by the waves' shared third entries and the final union
-  // of their lists (measured: filling the first KB = 20 at once cost about
-  // 4 us per launch, eight per later chunk about 0.5 us).
+  // first chunks at the start most of all). Early on the list is short, so
+  // the waves' first chunks meet no bound and are deferred (kept in LDS);
+  // the bound builds up from the waves' shared ceil(KB/8)-th entries, and
+  // the final one comes from the union of their lists. (On 256 x 248,320
+  // logits with KB = 20, inserting the first chunk's top KB at once cost
+  // about 4 us per launch, eight per later chunk about 0.5 us.)
   const int r_first = plan.KB < 2 ? plan.KB : 2;
   const int r_next = r_first;
 
