@@ -8,8 +8,11 @@
  *   crates/yskn-ref/src/portable_math.rs:52-58,224-364   exp_d, log_d
  *   crates/yskn-ref/src/output_head_sampler.rs:21-250     sampler, NLL
  *   crates/yskn-ref/src/speculation.rs:483-523            acceptance loop
- *   crates/yskn-ref/src/draft_head.rs:325-379             draft coupling
- *   docs/spec/06_OUTPUT_HEAD_SAMPLER.md:99-230            normative text
+ *   crates/yskn-ref/src/draft_head.rs:219-379             draft shortlist, top 16, coupling
+ *   crates/yskn-ref/src/portable_math.rs:61-111           sqrt_rn, rsqrt
+ *   crates/yskn-ref/src/residual_norm_mlp.rs:37-46        inverse RMS of the head input
+ *   crates/yskn-ref/src/compressed_linear.rs:329-340      head scale restoration
+ *   docs/spec/06_OUTPUT_HEAD_SAMPLER.md:21-230            normative text
  *
  * Compile with -ffp-contract=off and without -ffast-math: each binary64
  * multiply and add below must round separately.
@@ -372,7 +375,7 @@ static int truncate_candidates(const float* logits, const uint32_t* cands, uint6
 }
 
 static int draw(const uint32_t* cands, const truncation* tr, uint64_t position,
-                const yo_params* p, uint64_t* pick) {
+                const yo_params* p, uint64_t* pick, yo_diag* diag) {
   uint64_t selected = tr->retained - 1;
   if (p->version == YO_VERSION_GUMBEL) {
     double best = -INFINITY;
@@ -389,6 +392,11 @@ static int draw(const uint32_t* cands, const truncation* tr, uint64_t position,
     for (uint64_t j = 0; j < tr->retained; ++j) mass = mass + tr->weights[j];
     const double uniform = yo_uniform_v2(p->seed, position);
     const double threshold = uniform * mass;
+    if (diag) {
+      diag->kept = mass;
+      diag->uniform = uniform;
+      diag->threshold = threshold;
+    }
     double prefix = 0.0;
     for (uint64_t j = 0; j < tr->retained; ++j) {
       prefix = prefix + tr->weights[j];
@@ -419,7 +427,12 @@ int yo_sample(const float* logits, uint64_t V, uint64_t position, const yo_param
   truncation tr = {0};
   st = truncate_candidates(logits, cands, k, p, &tr);
   uint64_t pick = 0;
-  if (!st) st = draw(cands, &tr, position, p, &pick);
+  if (diag) {
+    diag->kept = 0.0;
+    diag->uniform = 0.0;
+    diag->threshold = 0.0;
+  }
+  if (!st) st = draw(cands, &tr, position, p, &pick, diag);
   if (!st) {
     *out = cands[pick];
     if (diag) {
@@ -448,7 +461,7 @@ int yo_sample_positions(const float* logits, uint64_t V, const uint64_t* positio
   st = truncate_candidates(logits, cands, k, p, &tr);
   for (uint64_t i = 0; !st && i < n; ++i) {
     uint64_t pick = 0;
-    st = draw(cands, &tr, positions[i], p, &pick);
+    st = draw(cands, &tr, positions[i], p, &pick, NULL);
     if (!st) out[i] = cands[pick];
   }
   free_truncation(&tr);
@@ -552,6 +565,8 @@ int yo_verify(const float* rows, uint64_t M, uint64_t V, uint64_t ld, const uint
   uint64_t em = 0, acc = 0;
   int eos = 0;
   for (uint64_t row = 0; row < M; ++row) {
+    /* checked_add: no wrap past 2^64 - 1 (speculation.rs:489-497) */
+    if (base_position > UINT64_MAX - (row + 1)) return YO_EINVAL;
     const uint64_t pos = base_position + row + 1;
     uint32_t sel = 0;
     int st = greedy ? yo_greedy(rows + row * ld, V, &sel)
@@ -574,17 +589,23 @@ int yo_verify(const float* rows, uint64_t M, uint64_t V, uint64_t ld, const uint
 /* ------------------------------------------------------------------------ */
 /* Draft coupling: draft_head.rs:325-379.                                    */
 /* ------------------------------------------------------------------------ */
-int yo_draft_choose(const float* scores, const uint32_t* tokens, uint64_t seed,
-                    uint32_t temperature_thousandths, uint64_t position, uint32_t* out) {
+int yo_draft_choose_ex(const float* scores, const uint32_t* tokens, int greedy, uint64_t seed,
+                       uint32_t temperature_thousandths, uint64_t position, uint32_t* out,
+                       yo_draft_diag* diag) {
   for (int i = 0; i < 16; ++i)
     if (!f32_finite(scores[i])) return YO_EINVAL;
-  if (temperature_thousandths == 0) return YO_EINVAL;
+  /* greedy part: first strictly larger score in input order (:331-336) */
   int best = 0;
   for (int i = 1; i < 16; ++i)
     if (scores[i] > scores[best]) best = i;
+  if (greedy) {
+    *out = tokens[best];
+    return YO_OK;
+  }
+  if (temperature_thousandths == 0) return YO_EINVAL;
   int order[16];
   for (int i = 0; i < 16; ++i) order[i] = i;
-  /* insertion sort by (score desc, token asc); 16 entries */
+  /* insertion sort by (score desc, token asc); 16 entries (:346-353) */
   for (int i = 1; i < 16; ++i) {
     int o = order[i], j = i;
     while (j > 0) {
@@ -596,7 +617,7 @@ int yo_draft_choose(const float* scores, const uint32_t* tokens, uint64_t seed,
     }
     order[j] = o;
   }
-  /* binary64 multiply by 0.001, not division (draft_head.rs:353-354) */
+  /* binary64 multiply by 0.001, not division (draft_head.rs:354-355) */
   const double temperature = 0.001 * (double)temperature_thousandths;
   double z[16], w[16];
   for (int i = 0; i < 16; ++i) {
@@ -607,10 +628,13 @@ int yo_draft_choose(const float* scores, const uint32_t* tokens, uint64_t seed,
   double total = 0.0;
   for (int i = 0; i < 16; ++i) total = total + w[order[i]];
   double prefix = 0.0, maximum = -INFINITY;
+  int member[16] = {0};
   for (int t = 0; t < 16; ++t) {
     const int i = order[t];
+    /* membership is decided before this candidate's weight is added (:368-377) */
     double lim = 0.95 * total;
     if (prefix < lim) {
+      member[i] = 1;
       double score = z[i] + yo_gumbel(seed, position, tokens[i]);
       if (score > maximum) {
         maximum = score;
@@ -619,6 +643,210 @@ int yo_draft_choose(const float* scores, const uint32_t* tokens, uint64_t seed,
     }
     prefix = prefix + w[i];
   }
+  if (diag) {
+    diag->temperature = temperature;
+    diag->total = total;
+    for (int i = 0; i < 16; ++i) {
+      diag->z[i] = z[i];
+      diag->w[i] = w[i];
+      diag->order[i] = order[i];
+      diag->member[i] = member[i];
+    }
+  }
   *out = tokens[best];
   return YO_OK;
+}
+
+int yo_draft_choose(const float* scores, const uint32_t* tokens, uint64_t seed,
+                    uint32_t temperature_thousandths, uint64_t position, uint32_t* out) {
+  return yo_draft_choose_ex(scores, tokens, 0, seed, temperature_thousandths, position, out, NULL);
+}
+
+/* ------------------------------------------------------------------------ */
+/* Draft shortlist and top 16: draft_head.rs:219-300.                        */
+/* ------------------------------------------------------------------------ */
+/* Order-preserving key without canonicalising -0 (draft_head.rs:219-226). */
+static inline uint32_t draft_key(float x) {
+  const uint32_t u = f32_bits(x);
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
+/* Highest bin b with (count of bins > b) + hist[b] >= need; *above = count of
+ * bins > b (draft_head.rs:227-236). */
+static uint64_t cutoff_bin(const uint64_t* hist, uint64_t nbins, uint64_t need, uint64_t* above) {
+  uint64_t a = 0;
+  for (uint64_t b = nbins; b-- > 0;) {
+    if (a + hist[b] >= need) {
+      *above = a;
+      return b;
+    }
+    a += hist[b];
+  }
+  *above = a;
+  return 0;
+}
+
+int yo_shortlist(const float* scores, uint64_t V, uint64_t count, uint32_t* out) {
+  for (uint64_t i = 0; i < V; ++i)
+    if (!f32_finite(scores[i])) return YO_ENONFINITE;
+  if (count < 16 || count > 2048 || count % 8 != 0 || count > V || V > 0x7fffffffull)
+    return YO_EINVAL;
+  uint64_t* h1 = (uint64_t*)calloc(1024, sizeof(uint64_t));
+  uint64_t* h2 = (uint64_t*)calloc(2048, sizeof(uint64_t));
+  if (!h1 || !h2) {
+    free(h1);
+    free(h2);
+    return YO_EINVAL;
+  }
+  for (uint64_t i = 0; i < V; ++i) h1[draft_key(scores[i]) >> 22] += 1;
+  uint64_t above1 = 0, above2 = 0;
+  const uint64_t first = cutoff_bin(h1, 1024, count, &above1);
+  for (uint64_t i = 0; i < V; ++i) {
+    const uint32_t k = draft_key(scores[i]);
+    if ((uint64_t)(k >> 22) == first) h2[(k >> 11) & 2047u] += 1;
+  }
+  const uint64_t second = cutoff_bin(h2, 2048, count - above1, &above2);
+  const uint32_t prefix = (uint32_t)((first << 11) | second);
+  uint64_t n = 0;
+  for (uint64_t i = 0; i < V; ++i)
+    if ((draft_key(scores[i]) >> 11) > prefix) out[n++] = (uint32_t)i;
+  for (uint64_t i = 0; i < V && n < count; ++i)
+    if ((draft_key(scores[i]) >> 11) == prefix) out[n++] = (uint32_t)i;
+  free(h1);
+  free(h2);
+  return n == count ? YO_OK : YO_EINVAL;
+}
+
+int yo_top16(const uint32_t* tokens, const float* scores, uint64_t n, uint32_t* out_tokens,
+             float* out_scores) {
+  if (n < 16) return YO_EINVAL;
+  for (uint64_t i = 0; i < n; ++i)
+    if (!f32_finite(scores[i])) return YO_EINVAL;
+  uint64_t* idx = (uint64_t*)malloc(n * sizeof(uint64_t));
+  if (!idx) return YO_EINVAL;
+  for (uint64_t i = 0; i < n; ++i) idx[i] = i;
+  /* insertion sort by (score desc, token asc): n is a shortlist (<= 2048) */
+  for (uint64_t i = 1; i < n; ++i) {
+    const uint64_t o = idx[i];
+    uint64_t j = i;
+    while (j > 0) {
+      const uint64_t q = idx[j - 1];
+      const int before = scores[o] > scores[q] || (scores[o] == scores[q] && tokens[o] < tokens[q]);
+      if (!before) break;
+      idx[j] = q;
+      --j;
+    }
+    idx[j] = o;
+  }
+  /* distinct tokens are required (draft_head.rs:292-299): equal tokens end up
+   * adjacent only when their scores are equal too, so compare every pair */
+  int dup = 0;
+  for (uint64_t i = 0; i < n && !dup; ++i)
+    for (uint64_t j = i + 1; j < n; ++j)
+      if (tokens[i] == tokens[j]) {
+        dup = 1;
+        break;
+      }
+  if (!dup) {
+    for (int i = 0; i < 16; ++i) {
+      out_tokens[i] = tokens[idx[i]];
+      out_scores[i] = scores[idx[i]];
+    }
+  }
+  free(idx);
+  return dup ? YO_EINVAL : YO_OK;
+}
+
+/* ------------------------------------------------------------------------ */
+/* Head epilogue: spec 06 section 2; compressed_linear.rs:329-340;          */
+/* residual_norm_mlp.rs:37-46; portable_math.rs:61-111.                      */
+/* ------------------------------------------------------------------------ */
+/* Correctly rounded binary32 square root from an integer square root: for a
+ * normalised radicand m * 2^(2e) with m < 2^48, r = isqrt(m) has 24 or 25
+ * significant bits; the remainder m - r^2 decides round-to-nearest exactly
+ * (a halfway case would need m = (r + 1/2)^2, impossible for an integer m). */
+static uint64_t isqrt_u64(uint64_t m) {
+  uint64_t r = 0, bit = 1ull << 62;
+  while (bit > m) bit >>= 2;
+  while (bit) {
+    if (m >= r + bit) {
+      m -= r + bit;
+      r = (r >> 1) + bit;
+    } else {
+      r >>= 1;
+    }
+    bit >>= 2;
+  }
+  return r;
+}
+
+float yo_sqrt_rn(float value) {
+  const uint32_t b = f32_bits(value);
+  if ((b & 0x7fffffffu) == 0 || b == 0x7f800000u) return value; /* +-0, +inf */
+  if ((b & 0x80000000u) || (b & 0x7f800000u) == 0x7f800000u) return NAN;
+  uint64_t sig;
+  int e; /* value = sig * 2^e */
+  if ((b >> 23) == 0) {
+    sig = b & 0x007fffffu;
+    e = -149;
+  } else {
+    sig = (b & 0x007fffffu) | 0x00800000u;
+    e = (int)(b >> 23) - 150;
+  }
+  /* scale sig to [2^46, 2^48) with an even exponent */
+  int lz = __builtin_clzll(sig); /* sig < 2^24 */
+  int shift = (63 - lz <= 46) ? (46 - (63 - lz)) : 0;
+  int ee = e - shift;
+  if (ee & 1) {
+    shift += 1;
+    ee -= 1;
+  }
+  const uint64_t m = sig << shift; /* m in [2^46, 2^48) */
+  uint64_t r = isqrt_u64(m);        /* in [2^23, 2^24] */
+  const uint64_t rem = m - r * r;
+  if (rem > r) r += 1;              /* m - r^2 > r + 1/4 <=> m > (r + 1/2)^2 */
+  int ex = ee / 2;                  /* sqrt(value) ~ r * 2^ex */
+  if (r == (1ull << 24)) {
+    r >>= 1;
+    ex += 1;
+  }
+  /* r in [2^23, 2^24): value bits = (ex + 23 + 127) << 23 | (r - 2^23) */
+  const uint32_t out = ((uint32_t)(ex + 23 + 127) << 23) | ((uint32_t)r & 0x007fffffu);
+  float f;
+  memcpy(&f, &out, 4);
+  return f;
+}
+
+float yo_rsqrt(float value) {
+  volatile float s = yo_sqrt_rn(value);
+  return 1.0f / s;
+}
+
+int yo_inverse_rms(const float* block_sums, uint64_t n_blocks, float width, float epsilon,
+                   float* out) {
+  float total = 0.0f;
+  for (uint64_t b = 0; b < n_blocks; ++b) total = total + block_sums[b];
+  if (!f32_finite(total)) return YO_ENONFINITE;
+  float q = total / width;
+  float arg = q + epsilon;
+  if (!f32_finite(arg)) return YO_ENONFINITE;
+  float r = yo_rsqrt(arg);
+  if (!f32_finite(r)) return YO_ENONFINITE;
+  *out = r;
+  return YO_OK;
+}
+
+int yo_head_logits(const int64_t* acc, const float* tau, uint64_t V, float unit_scale,
+                   float inverse_rms, float* out) {
+  if (!f32_finite(inverse_rms)) return YO_ENONFINITE;
+  int bad = 0;
+  for (uint64_t v = 0; v < V; ++v) {
+    float x = (float)acc[v]; /* one round-to-nearest conversion */
+    x = x * unit_scale;
+    x = x * inverse_rms;
+    x = x * tau[v];
+    out[v] = x;
+    bad |= !f32_finite(x);
+  }
+  return bad ? YO_ENONFINITE : YO_OK;
 }

@@ -11,7 +11,7 @@
  * semantics are defined here and are "parity unpinned" against the reference
  * (they are pinned only by the properties the tests check).
  *
- * Build: plain C11, -O2 -ffp-contract=off, no -ffast-math. Every binary64
+ * Build: plain C11, -O3 -ffp-contract=off, no -ffast-math. Every binary64
  * operation is a separately rounded IEEE operation, as the reference's
  * portable math requires (crates/yskn-ref/src/portable_math.rs:1-7).
  */
@@ -52,6 +52,9 @@ typedef struct yo_diag {
   uint64_t retained; /* retained after min-p */
   uint64_t pick;     /* selected candidate index */
   double total;      /* serial binary64 total of the top-k weights */
+  double kept;       /* version 2: serial binary64 mass of the retained weights */
+  double uniform;    /* version 2: the position-keyed uniform */
+  double threshold;  /* version 2: uniform * kept */
 } yo_diag;
 
 /* ---- portable math (portable_math.rs:224-364) ---------------------------- */
@@ -107,6 +110,9 @@ int yo_apply_penalties(float* logits, uint64_t V, const uint32_t* history, uint6
  * first mismatch or EOS); *emitted = number of tokens pushed; *accepted = number
  * of guesses that matched among emitted rows; *stop_eos = 1 if an EOS stopped it.
  * greedy != 0 uses Greedy instead of the sampler. */
+/* A prediction position past 2^64 - 1 fails with YO_EINVAL when the loop
+ * reaches its row (speculation.rs:489-497); rows after the first mismatch are
+ * never sampled, so their logits are never validated (:520-522). */
 int yo_verify(const float* rows, uint64_t M, uint64_t V, uint64_t ld, const uint32_t* guesses,
               uint64_t base_position, const yo_params* p, int greedy, const uint32_t* eos_ids,
               uint64_t n_eos, uint32_t* selected, uint64_t* emitted, uint64_t* accepted,
@@ -116,6 +122,50 @@ int yo_verify(const float* rows, uint64_t M, uint64_t V, uint64_t ld, const uint
 /* Sampled choice among 16 draft candidates with Gumbel coupling. */
 int yo_draft_choose(const float* scores, const uint32_t* tokens, uint64_t seed,
                     uint32_t temperature_thousandths, uint64_t position, uint32_t* out);
+
+/* Intermediates of one draft choice, for pinning the arithmetic. */
+typedef struct yo_draft_diag {
+  double temperature; /* 0.001 * thousandths (binary64 multiply) */
+  double z[16];       /* (score_i - score_top) / temperature, input order */
+  double w[16];       /* exp_d(z_i), input order */
+  double total;       /* serial sum of w in (score desc, token asc) order */
+  int order[16];      /* input indices in (score desc, token asc) order */
+  int member[16];     /* 1 if candidate i entered the Gumbel argmax */
+} yo_draft_diag;
+/* greedy != 0: DraftChoice::Greedy (first highest score in input order);
+ * otherwise DraftChoice::Sampled { seed, temperature_thousandths }. diag may be
+ * NULL (it is filled only for a sampled choice). */
+int yo_draft_choose_ex(const float* scores, const uint32_t* tokens, int greedy, uint64_t seed,
+                       uint32_t temperature_thousandths, uint64_t position, uint32_t* out,
+                       yo_draft_diag* diag);
+
+/* ---- draft shortlist and top 16 (draft_head.rs:219-300) ------------------ */
+/* Two-stage histogram cutoff over order-preserving keys (1,024 bins of
+ * key >> 22, then 2,048 bins of (key >> 11) & 2047 inside the cutoff bin);
+ * ids above the cutoff prefix in ascending id order, then cutoff-prefix ids in
+ * ascending id order until `count` (16..2048, multiple of 8, <= V). */
+int yo_shortlist(const float* scores, uint64_t V, uint64_t count, uint32_t* out);
+/* The 16 best of n >= 16 distinct (token, score) candidates in
+ * (score desc, token asc) order. */
+int yo_top16(const uint32_t* tokens, const float* scores, uint64_t n, uint32_t* out_tokens,
+             float* out_scores);
+
+/* ---- head epilogue (spec 06 section 2; compressed_linear.rs:311-346;
+ *      residual_norm_mlp.rs:37-46; portable_math.rs:61-111) ---------------- */
+/* Correctly rounded binary32 square root (portable_math.rs:61-106). */
+float yo_sqrt_rn(float value);
+/* 1 / sqrt_rn(value), the division rounded separately (portable_math.rs:108-111). */
+float yo_rsqrt(float value);
+/* inverse_rms = rsqrt(fold_add32(block_sums[0..n_blocks]) / width + epsilon),
+ * the fold starting from +0 (residual_norm_mlp.rs:37-46). Returns YO_ENONFINITE
+ * if the sum, the argument or the result is not finite. */
+int yo_inverse_rms(const float* block_sums, uint64_t n_blocks, float width, float epsilon,
+                   float* out);
+/* logit[v] = ((float)acc[v] * unit_scale) * inverse_rms * tau[v], each product
+ * a separately rounded binary32 multiply, one RN int64 -> binary32 conversion
+ * (compressed_linear.rs:329-340). YO_ENONFINITE if any logit is not finite. */
+int yo_head_logits(const int64_t* acc, const float* tau, uint64_t V, float unit_scale,
+                   float inverse_rms, float* out);
 
 #ifdef __cplusplus
 }

@@ -40,6 +40,22 @@ class Diag(C.Structure):
         ("retained", C.c_uint64),
         ("pick", C.c_uint64),
         ("total", C.c_double),
+        ("kept", C.c_double),
+        ("uniform", C.c_double),
+        ("threshold", C.c_double),
+    ]
+
+
+class DraftDiag(C.Structure):
+    """yo_draft_diag: intermediates of one sampled draft choice."""
+
+    _fields_ = [
+        ("temperature", C.c_double),
+        ("z", C.c_double * 16),
+        ("w", C.c_double * 16),
+        ("total", C.c_double),
+        ("order", C.c_int * 16),
+        ("member", C.c_int * 16),
     ]
 
 
@@ -90,6 +106,15 @@ def lib() -> C.CDLL:
                                 C.POINTER(C.c_int)]
         L.yo_draft_choose.argtypes = [f32p, u32p, C.c_uint64, C.c_uint32, C.c_uint64,
                                       C.POINTER(C.c_uint32)]
+        L.yo_draft_choose_ex.argtypes = [f32p, u32p, C.c_int, C.c_uint64, C.c_uint32, C.c_uint64,
+                                         C.POINTER(C.c_uint32), C.POINTER(DraftDiag)]
+        L.yo_shortlist.argtypes = [f32p, C.c_uint64, C.c_uint64, u32p]
+        L.yo_top16.argtypes = [u32p, f32p, C.c_uint64, u32p, f32p]
+        L.yo_sqrt_rn.argtypes, L.yo_sqrt_rn.restype = [C.c_float], C.c_float
+        L.yo_rsqrt.argtypes, L.yo_rsqrt.restype = [C.c_float], C.c_float
+        L.yo_inverse_rms.argtypes = [f32p, C.c_uint64, C.c_float, C.c_float, C.POINTER(C.c_float)]
+        i64p = np.ctypeslib.ndpointer(np.int64, flags="C_CONTIGUOUS")
+        L.yo_head_logits.argtypes = [i64p, f32p, C.c_uint64, C.c_float, C.c_float, f32p]
         _lib = L
     return _lib
 
@@ -228,3 +253,57 @@ def draft_choose(scores, tokens, seed: int, temperature_thousandths: int, positi
     out = C.c_uint32()
     _check(lib().yo_draft_choose(s, t, seed, temperature_thousandths, position, C.byref(out)))
     return out.value
+
+
+def draft_choose_ex(scores, tokens, seed: int, temperature_thousandths: int, position: int,
+                    greedy: bool = False):
+    """DraftChoice::{Greedy, Sampled} (draft_head.rs:325-379); returns (token, diag)."""
+    s = _f32(scores)
+    t = np.ascontiguousarray(tokens, dtype=np.uint32)
+    out = C.c_uint32()
+    d = DraftDiag()
+    _check(lib().yo_draft_choose_ex(s, t, 1 if greedy else 0, seed, temperature_thousandths, position,
+                                    C.byref(out), C.byref(d)))
+    return out.value, d
+
+
+def shortlist(scores, count: int) -> np.ndarray:
+    """draft_head.rs:239-282: two-stage histogram cutoff, ascending-id tie bucket."""
+    s = _f32(scores)
+    out = np.zeros(count, np.uint32)
+    _check(lib().yo_shortlist(s, s.size, count, out))
+    return out
+
+
+def top16(tokens, scores):
+    """draft_head.rs:284-300: the 16 best (score desc, token asc)."""
+    t = np.ascontiguousarray(tokens, dtype=np.uint32)
+    s = _f32(scores)
+    ot = np.zeros(16, np.uint32)
+    os_ = np.zeros(16, np.float32)
+    _check(lib().yo_top16(t, s, t.size, ot, os_))
+    return ot, os_
+
+
+def sqrt_rn(x: float) -> float:
+    return lib().yo_sqrt_rn(x)
+
+
+def rsqrt(x: float) -> float:
+    return lib().yo_rsqrt(x)
+
+
+def inverse_rms(block_sums, width: float, epsilon: float) -> float:
+    b = _f32(block_sums)
+    out = C.c_float()
+    _check(lib().yo_inverse_rms(b, b.size, width, epsilon, C.byref(out)))
+    return out.value
+
+
+def head_logits(acc, tau, unit_scale: float, inv_rms: float) -> np.ndarray:
+    """Head scale restoration (compressed_linear.rs:329-340; spec 06 section 2)."""
+    a = np.ascontiguousarray(acc, dtype=np.int64)
+    t = _f32(tau)
+    out = np.zeros(a.size, np.float32)
+    _check(lib().yo_head_logits(a, t, a.size, unit_scale, inv_rms, out))
+    return out
