@@ -112,12 +112,26 @@ typedef struct yskn_smp_aux {
   uint32_t* logprob_ids; /* [rows*n_logprobs] */
   double* logprobs;      /* [rows*n_logprobs] */
   int32_t* row_status;   /* [rows] per-row YSKN_SMP_* status */
-  /* EXTENSION: token history for the penalties (row r uses
-   * history[r*history_ld .. + history_len[r]]). */
+  /* EXTENSION: token history for the penalties: row r uses
+   * history[r*history_ld .. + history_len[r]]. history_ld = 0 shares one
+   * history among all rows; history_ld < 0 is rejected. A row whose
+   * history_len is negative, above 16,384, above a positive history_ld, or
+   * that holds an id >= vocab fails with YSKN_SMP_EINVAL. The caller must
+   * size the buffer for the rows' lengths. */
   const uint32_t* history;
   const int32_t* history_len; /* [rows] */
   int64_t history_ld;
 } yskn_smp_aux;
+
+/* Device-side position/token advance: the reference sampler's adv_pos /
+ * adv_tok (src/q35.hpp:118; src/q35_sample.cu:206) and Engine35::commit
+ * (src/engine35.cpp:1319-1329) without a host round trip. Both pointers are
+ * device pointers; `position` may be the same counter the call reads its
+ * base position from (it is read before it is advanced). */
+typedef struct yskn_smp_advance {
+  uint64_t* position; /* advanced by the number of tokens emitted */
+  uint32_t* token;    /* set to the last emitted token */
+} yskn_smp_advance;
 
 /* Result of a speculative verification; mirrors the accept loop of
  * crates/yskn-ref/src/speculation.rs:483-523 and src/specx.cpp:376-440. */
@@ -126,6 +140,9 @@ typedef struct yskn_smp_verify_result {
   uint32_t emitted;  /* tokens produced: accepted drafts + correction or bonus */
   uint32_t token;    /* last emitted token: the correction, or the bonus token */
   int32_t stop_eos;  /* 1 if an EOS id ended the pass */
+  /* YSKN_SMP_OK, or the status of the first row the accept walk reached that
+   * failed (then accepted = emitted = 0 and token = 0xFFFFFFFF) */
+  int32_t status;
 } yskn_smp_verify_result;
 
 /* Thread-local description of the last failure on this thread
@@ -169,6 +186,24 @@ int yskn_smp_sample(yskn_smp_handle h, const void* logits, int32_t dtype, int32_
                     int32_t vocab, int64_t ld, const uint64_t* positions, int32_t n_draws,
                     uint32_t* out_ids, const yskn_smp_aux* aux, void* stream);
 
+/* Sample one token per row at device-resident positions: the position form
+ * and advance of launch_q35_smp (src/q35_sample.cu:180-181,206;
+ * Q35SmpArgs d_pos / wk / row0 / adv_pos / adv_tok, src/q35.hpp:117-118).
+ * Row r is sampled at prediction position
+ *     *base_position + depth + 1,  depth = row_depth ? row_depth[row0 + r] : row0 + r
+ * with checked unsigned 64-bit arithmetic: a position past 2^64 - 1 fails the
+ * row with YSKN_SMP_EINVAL (speculation.rs:489-497). One draw per row.
+ *   base_position  device [1]
+ *   row_depth      device [row0 + rows] depth table (may be NULL)
+ *   advance        optional (may be NULL): only for rows = 1; after the row is
+ *                  sampled, *advance->position += 1 and *advance->token = id
+ *                  (a failed row advances nothing).
+ * Asynchronous on `stream`, like yskn_smp_sample. */
+int yskn_smp_sample_at(yskn_smp_handle h, const void* logits, int32_t dtype, int32_t rows,
+                       int32_t vocab, int64_t ld, const uint64_t* base_position,
+                       const uint8_t* row_depth, int32_t row0, uint32_t* out_ids,
+                       const yskn_smp_aux* aux, const yskn_smp_advance* advance, void* stream);
+
 /* Greedy argmax per row: greedy() (output_head_sampler.rs:103-113),
  * launch_argmax (src/args.hpp:24-30; src/misc_kernels.cu:57-96).
  * Like the two entry points below, a pure function of the logits: the
@@ -191,21 +226,32 @@ int yskn_smp_nll(yskn_smp_handle h, const void* logits, int32_t dtype, int32_t r
                  void* stream);
 
 /* One-launch speculative verification of M rows: row j is sampled at
- * prediction position *base_position + j + 1 with the row-0 parameters,
+ * prediction position *base_position + j + 1 (checked like the reference's
+ * accept loop) with the handle's parameters (one set, or one per row),
  * drafts[j] (j < M-1) is accepted while it equals the selected token, and the
  * first mismatch's selection (or the bonus when all match) ends the pass; an
- * EOS id among the emitted tokens stops it. Replaces the per-row Selector loop
- * of speculation.rs:483-523 and the host accept loop of src/specx.cpp:376-440.
+ * EOS id among the emitted tokens stops it. A failed row (non-finite logits,
+ * position overflow, invalid history) fails the pass only when the walk
+ * reaches it. Replaces the per-row Selector loop of speculation.rs:483-523,
+ * the host accept loop of src/specx.cpp:376-440 and, with `commit`, the
+ * commit of Engine35::commit (src/engine35.cpp:1319-1329).
  *   target_logits device [M x ld]; drafts device [M-1]; base_position device [1]
  *   eos_ids device [n_eos] (may be NULL when n_eos = 0)
- *   out_ids device [M] selected token per row; result device [1] */
+ *   out_ids device [M] selected token per row; result device [1]
+ *   aux     optional per-row outputs of yskn_smp_sample (argmax, top-8,
+ *           top-20, logprobs, row status: yskn_verify's out_argmax / top_ids /
+ *           top_vals, include/yskn_abi.h:39,55) and the penalty history
+ *   commit  optional: when the pass succeeds, *commit->position += emitted
+ *           and *commit->token = the last emitted token */
 int yskn_smp_verify(yskn_smp_handle h, const void* target_logits, int32_t dtype, int32_t M,
                     int32_t vocab, int64_t ld, const uint32_t* drafts,
                     const uint64_t* base_position, const uint32_t* eos_ids, int32_t n_eos,
-                    uint32_t* out_ids, yskn_smp_verify_result* result, void* stream);
+                    uint32_t* out_ids, yskn_smp_verify_result* result, const yskn_smp_aux* aux,
+                    const yskn_smp_advance* commit, void* stream);
 
 /* Synchronise `stream` and return the first per-row error of the handle's
- * last call (YSKN_SMP_OK if none), setting yskn_smp_last_error(). */
+ * last call (YSKN_SMP_OK if none), setting yskn_smp_last_error(). After a
+ * verify it returns the pass's status (yskn_smp_verify_result.status). */
 int yskn_smp_sync(yskn_smp_handle h, void* stream);
 
 /* Host-slice convenience with the exact signature semantics of the Rust
@@ -230,6 +276,20 @@ int yskn_smp_validate_params(const yskn_smp_params* params, int32_t vocab, uint3
 /* The same for binary64 parameters (SamplingParameters::validate on the
  * Rust fields as they are, NaN and infinities included). */
 int yskn_smp_validate_params_f64(const yskn_smp_params_f64* params, int32_t vocab, uint32_t flags);
+
+/* Device-math test hook, the counterpart of the reference's yskn_pm_test
+ * (src/pm_test.cu:30-52): evaluates one device primitive of the sampler on n
+ * inputs (host buffers in and out; the call synchronises).
+ *   fn 10: exp_d   binary64 -> binary64   (portable_math.rs:224-283)
+ *   fn 11: log_d   binary64 -> binary64   (portable_math.rs:297-364)
+ *   fn 12: gumbel  (seed, position, token) u64 triples -> binary64
+ *                  (output_head_sampler.rs:221-228)
+ *   fn 13: version-2 uniform (seed, position) u64 pairs -> binary64 (:196-197)
+ *   fn 14: mix64   u64 -> u64 (:214-219)
+ *   fn 6:  rsqrt   binary32 bits base + i -> binary32 bits (portable_math.rs:108-111)
+ *   fn 7:  sqrt_rn binary32 bits base + i -> binary32 bits (portable_math.rs:61-106)
+ * n in 1..2^28. Returns 0 or a negative status. */
+int yskn_smp_pm_test(int32_t fn, uint64_t base, const void* host_in, void* host_out, int64_t n);
 
 /* Library version string. */
 const char* yskn_smp_version(void);

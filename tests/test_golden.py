@@ -243,7 +243,8 @@ def test_device_matches_verify_fixture(case):
         ids, res, _keep = dev.verify(torch.from_numpy(target).cuda(), torch.tensor(vc["drafts"]).cuda(),
                                      torch.tensor([vc["base_position"]]).cuda(), vc["eos"])
         dev.sync()
-        accepted, emitted, token, stop = res.cpu().tolist()
+        accepted, emitted, token, stop, status = res.cpu().tolist()
+        assert status == 0
         assert (accepted, emitted, bool(stop)) == (vc["accepted"], vc["emitted"], vc["stop_eos"])
         assert ids.cpu().tolist()[:emitted] == vc["selected"]
         assert token == vc["selected"][-1]

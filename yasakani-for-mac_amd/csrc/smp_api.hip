@@ -60,6 +60,8 @@ struct yskn_smp {
   uint64_t* d_host_pos = nullptr;
   uint32_t* d_host_out = nullptr;
   int32_t last_rows = 0;
+  // the last call was a verify: its pass status is in the caller's result
+  const yskn_smp_verify_result* last_verify = nullptr;
 };
 
 namespace {
@@ -85,6 +87,10 @@ bool finite_f(float x) {
   return (b & 0x7f800000u) != 0x7f800000u;
 }
 
+// |l - M| <= 2 * FLT_MAX for finite binary32 logits, so (l - M) / T cannot
+// overflow binary64 unless T < 2 * FLT_MAX / DBL_MAX ~ 3.8e-270.
+bool needs_zcheck(const DevParams& d) { return !d.greedy && d.temperature < 1e-260; }
+
 DevParams to_device(const yskn_smp_params& p) {
   DevParams d;
   std::memset(&d, 0, sizeof d);
@@ -103,6 +109,7 @@ DevParams to_device(const yskn_smp_params& p) {
                 p.frequency_penalty != 0.0f)
                    ? 1
                    : 0;
+  d.zcheck = needs_zcheck(d) ? 1 : 0;
   return d;
 }
 
@@ -123,6 +130,7 @@ DevParams to_device(const yskn_smp_params_f64& p) {
                 p.frequency_penalty != 0.0f)
                    ? 1
                    : 0;
+  d.zcheck = needs_zcheck(d) ? 1 : 0;
   return d;
 }
 
@@ -213,6 +221,7 @@ SmpArgs base_args(yskn_smp_handle h, const void* logits, int32_t rows, int32_t v
   a.V = vocab;
   a.rows = rows;
   a.mode = MODE_SAMPLE;
+  a.pos_mode = POS_ARRAY;
   a.prm = h->d_params;
   a.prm_shared = h->params_shared ? 1 : 0;
   a.n_draws = 1;
@@ -260,6 +269,41 @@ int launch(yskn_smp_handle h, SmpArgs& a, int32_t dtype, bool pen, const yskn_sm
   hipError_t e = launch_sample(a, dtype == YSKN_SMP_F32 ? 0 : 1, a.vec != 0, pen, st);
   if (e != hipSuccess) return hip_fail(e, "sampler launch");
   h->last_rows = a.rows;
+  h->last_verify = a.mode == MODE_VERIFY ? (const yskn_smp_verify_result*)a.vresult : nullptr;
+  return YSKN_SMP_OK;
+}
+
+// The optional outputs and the penalty history of yskn_smp_aux into the
+// launch arguments; *pen tells whether the penalty kernel must run.
+int apply_aux(yskn_smp_handle h, SmpArgs& a, const yskn_smp_aux* aux, int32_t rows, bool* pen) {
+  *pen = false;
+  if (!aux) {
+    if (any_penalty(h, rows)) return fail(YSKN_SMP_EINVAL, "invalid input: penalties need a history");
+    return YSKN_SMP_OK;
+  }
+  if (aux->n_logprobs < 0 || aux->n_logprobs > KBMAX)
+    return fail(YSKN_SMP_EINVAL, "invalid input: n_logprobs must be in 0..=64");
+  if (aux->n_logprobs > 0 && (!aux->logprob_ids || !aux->logprobs))
+    return fail(YSKN_SMP_EINVAL, "invalid input: n_logprobs > 0 needs both output arrays");
+  if ((aux->top8_ids == nullptr) != (aux->top8_vals == nullptr) ||
+      (aux->top20_ids == nullptr) != (aux->top20_vals == nullptr))
+    return fail(YSKN_SMP_EINVAL, "invalid input: top lists need both ids and values");
+  a.argmax = aux->argmax;
+  a.top8_ids = aux->top8_ids;
+  a.top8_vals = aux->top8_vals;
+  a.top20_ids = aux->top20_ids;
+  a.top20_vals = aux->top20_vals;
+  a.n_lp = aux->n_logprobs;
+  a.lp_ids = aux->logprob_ids;
+  a.lp_vals = aux->logprobs;
+  a.row_status = aux->row_status;
+  a.want_mass = a.n_lp > 0 ? 1 : 0;
+  if (any_penalty(h, rows)) {
+    if (!aux->history || !aux->history_len)
+      return fail(YSKN_SMP_EINVAL, "invalid input: penalties need a history");
+    if (aux->history_ld < 0) return fail(YSKN_SMP_EINVAL, "invalid input: history_ld must be >= 0");
+    *pen = true;
+  }
   return YSKN_SMP_OK;
 }
 
@@ -396,32 +440,42 @@ int yskn_smp_sample(yskn_smp_handle h, const void* logits, int32_t dtype, int32_
   a.n_draws = n_draws < 1 ? 1 : n_draws;
   a.out_ids = out_ids;
   bool pen = false;
-  if (aux) {
-    if (aux->n_logprobs < 0 || aux->n_logprobs > KBMAX)
-      return fail(YSKN_SMP_EINVAL, "invalid input: n_logprobs must be in 0..=64");
-    if (aux->n_logprobs > 0 && (!aux->logprob_ids || !aux->logprobs))
-      return fail(YSKN_SMP_EINVAL, "invalid input: n_logprobs > 0 needs both output arrays");
-    if ((aux->top8_ids == nullptr) != (aux->top8_vals == nullptr) ||
-        (aux->top20_ids == nullptr) != (aux->top20_vals == nullptr))
-      return fail(YSKN_SMP_EINVAL, "invalid input: top lists need both ids and values");
-    a.argmax = aux->argmax;
-    a.top8_ids = aux->top8_ids;
-    a.top8_vals = aux->top8_vals;
-    a.top20_ids = aux->top20_ids;
-    a.top20_vals = aux->top20_vals;
-    a.n_lp = aux->n_logprobs;
-    a.lp_ids = aux->logprob_ids;
-    a.lp_vals = aux->logprobs;
-    a.row_status = aux->row_status;
-    a.want_mass = a.n_lp > 0 ? 1 : 0;
-    if (any_penalty(h, rows)) {
-      if (!aux->history || !aux->history_len)
-        return fail(YSKN_SMP_EINVAL, "invalid input: penalties need a history");
-      pen = true;
-    }
-  } else if (any_penalty(h, rows)) {
-    return fail(YSKN_SMP_EINVAL, "invalid input: penalties need a history");
+  st = apply_aux(h, a, aux, rows, &pen);
+  if (st) return st;
+  return launch(h, a, dtype, pen, aux, (hipStream_t)stream);
+}
+
+int yskn_smp_sample_at(yskn_smp_handle h, const void* logits, int32_t dtype, int32_t rows,
+                       int32_t vocab, int64_t ld, const uint64_t* base_position,
+                       const uint8_t* row_depth, int32_t row0, uint32_t* out_ids,
+                       const yskn_smp_aux* aux, const yskn_smp_advance* advance, void* stream) {
+  int st = check_common(h, logits, dtype, rows, vocab, ld);
+  if (st) return st;
+  if (!base_position || !out_ids)
+    return fail(YSKN_SMP_EINVAL, "invalid input: null base_position or out_ids");
+  if (row0 < 0) return fail(YSKN_SMP_EINVAL, "invalid input: row0 must be >= 0");
+  if (advance && (!advance->position || !advance->token))
+    return fail(YSKN_SMP_EINVAL, "invalid input: advance needs both a position and a token");
+  if (advance && rows != 1)
+    return fail(YSKN_SMP_EINVAL, "invalid input: advance is defined for one row");
+  if (!h->params_shared && rows > (int32_t)h->params.size())
+    return fail(YSKN_SMP_EINVAL, "invalid input: fewer per-row parameter sets than rows");
+  st = check_params_for(h, rows, vocab);
+  if (st) return st;
+  SmpArgs a = base_args(h, logits, rows, vocab, ld);
+  a.pos_mode = POS_BASE;
+  a.base_position = base_position;
+  a.row_depth = row_depth;
+  a.row0 = row0;
+  a.n_draws = 1;
+  a.out_ids = out_ids;
+  if (advance) {
+    a.adv_pos = advance->position;
+    a.adv_tok = advance->token;
   }
+  bool pen = false;
+  st = apply_aux(h, a, aux, rows, &pen);
+  if (st) return st;
   return launch(h, a, dtype, pen, aux, (hipStream_t)stream);
 }
 
@@ -466,20 +520,23 @@ int yskn_smp_nll(yskn_smp_handle h, const void* logits, int32_t dtype, int32_t r
 int yskn_smp_verify(yskn_smp_handle h, const void* target_logits, int32_t dtype, int32_t M,
                     int32_t vocab, int64_t ld, const uint32_t* drafts,
                     const uint64_t* base_position, const uint32_t* eos_ids, int32_t n_eos,
-                    uint32_t* out_ids, yskn_smp_verify_result* result, void* stream) {
+                    uint32_t* out_ids, yskn_smp_verify_result* result, const yskn_smp_aux* aux,
+                    const yskn_smp_advance* commit, void* stream) {
   int st = check_common(h, target_logits, dtype, M, vocab, ld);
   if (st) return st;
   if (!base_position || !out_ids || !result)
     return fail(YSKN_SMP_EINVAL, "invalid input: null base_position, out_ids or result");
   if (M > 1 && !drafts) return fail(YSKN_SMP_EINVAL, "invalid input: null drafts");
   if (n_eos < 0 || (n_eos > 0 && !eos_ids)) return fail(YSKN_SMP_EINVAL, "invalid input: eos ids");
-  if (any_penalty(h, M)) return fail(YSKN_SMP_EINVAL, "invalid input: penalties need yskn_smp_sample");
-  // verification uses the row-0 parameter set for every row
-  const int st2 = validate(h->params[0], vocab, h->flags);
-  if (st2) return st2;
+  if (commit && (!commit->position || !commit->token))
+    return fail(YSKN_SMP_EINVAL, "invalid input: commit needs both a position and a token");
+  if (!h->params_shared && M > (int32_t)h->params.size())
+    return fail(YSKN_SMP_EINVAL, "invalid input: fewer per-row parameter sets than rows");
+  st = check_params_for(h, M, vocab);
+  if (st) return st;
   SmpArgs a = base_args(h, target_logits, M, vocab, ld);
-  a.prm_shared = 1;
   a.mode = MODE_VERIFY;
+  a.pos_mode = POS_BASE;
   a.base_position = base_position;
   a.out_ids = out_ids;
   a.drafts = drafts;
@@ -487,7 +544,14 @@ int yskn_smp_verify(yskn_smp_handle h, const void* target_logits, int32_t dtype,
   a.n_eos = n_eos;
   a.vresult = (uint32_t*)result;
   a.vcount = h->d_vcount;
-  return launch(h, a, dtype, false, nullptr, (hipStream_t)stream);
+  if (commit) {
+    a.adv_pos = commit->position;
+    a.adv_tok = commit->token;
+  }
+  bool pen = false;
+  st = apply_aux(h, a, aux, M, &pen);
+  if (st) return st;
+  return launch(h, a, dtype, pen, aux, (hipStream_t)stream);
 }
 
 int yskn_smp_sync(yskn_smp_handle h, void* stream) {
@@ -499,9 +563,17 @@ int yskn_smp_sync(yskn_smp_handle h, void* stream) {
     e = hipMemcpy(s.data(), h->d_status, h->last_rows * sizeof(int32_t), hipMemcpyDeviceToHost);
     if (e != hipSuccess) return hip_fail(e, "yskn_smp_sync");
   }
+  if (h->last_verify) {
+    // a verify fails only on the rows its accept walk reached
+    yskn_smp_verify_result r;
+    e = hipMemcpy(&r, h->last_verify, sizeof r, hipMemcpyDeviceToHost);
+    if (e != hipSuccess) return hip_fail(e, "yskn_smp_sync");
+    s.assign(1, r.status);
+  }
   for (int32_t v : s) {
     if (v == YSKN_SMP_ENONFINITE) return fail(v, "non-finite value in logits");
-    if (v == YSKN_SMP_EINVAL) return fail(v, "invalid input: token outside the vocabulary");
+    if (v == YSKN_SMP_EINVAL)
+      return fail(v, "invalid input: token outside the vocabulary, invalid history or prediction position overflow");
     if (v != YSKN_SMP_OK) return fail(v, "sampler row failed");
   }
   return YSKN_SMP_OK;

@@ -49,7 +49,10 @@ struct DevParams {
   int32_t greedy;      // temperature_milli == 0
   int32_t penalize;    // any penalty active
   float rep, pres, freq;
-  int32_t pad;
+  // The temperature is so small that (l - M) / T can overflow binary64 for
+  // some finite binary32 logits: the row takes the exact dense path, which
+  // checks the weakest candidate's z like the reference does.
+  int32_t zcheck;
 };
 
 // Counters for profiling the path (cumulative since create).
@@ -63,6 +66,15 @@ enum StatIndex {
 
 enum Mode { MODE_SAMPLE = 0, MODE_VERIFY = 1 };
 
+// Where a row's prediction position comes from.
+enum PosMode {
+  POS_ARRAY = 0,  // positions[row * n_draws + d]
+  POS_BASE = 1,   // *base_position + depth + 1, depth = row_depth ? row_depth[row0 + row] : row0 + row
+};
+
+// Words of the verify result (the public yskn_smp_verify_result).
+enum VerifyWord { VR_ACCEPTED = 0, VR_EMITTED, VR_TOKEN, VR_STOP_EOS, VR_STATUS, VR_WORDS };
+
 struct SmpArgs {
   const void* logits;
   int64_t ld;  // elements between rows
@@ -72,8 +84,13 @@ struct SmpArgs {
   const DevParams* prm;
   int32_t prm_shared;
   int32_t n_draws;
-  const uint64_t* positions;     // [rows * n_draws] (sample mode)
-  const uint64_t* base_position; // verify mode: row j at *base + j + 1
+  int32_t pos_mode;              // PosMode
+  const uint64_t* positions;     // [rows * n_draws] (POS_ARRAY)
+  const uint64_t* base_position; // POS_BASE: row r at *base + depth(r) + 1
+  const uint8_t* row_depth;      // POS_BASE: optional depth table, indexed row0 + r
+  int32_t row0;
+  uint64_t* adv_pos;             // optional: advanced by the tokens emitted
+  uint32_t* adv_tok;             // optional: set to the last emitted token
   uint32_t* out_ids;             // [rows * n_draws] or NULL
   uint32_t* argmax;
   uint32_t* top8_ids;
@@ -109,7 +126,7 @@ struct SmpArgs {
   const uint32_t* drafts;
   const uint32_t* eos;
   int32_t n_eos;
-  uint32_t* vresult;  // 4 words: accepted, emitted, token, stop_eos
+  uint32_t* vresult;  // VR_WORDS words
   uint32_t* vcount;
 };
 

@@ -381,9 +381,23 @@ __device__ __forceinline__ RowPlan make_plan(const SmpArgs& A, const DevParams& 
   return p;
 }
 
-__device__ __forceinline__ uint64_t position_of(const SmpArgs& A, int row, int d) {
-  if (A.mode == MODE_VERIFY) return *A.base_position + (uint64_t)row + 1u;
+// Prediction position of draw d of a row. The base form is checked like the
+// reference's accept loop (checked_add, speculation.rs:489-497): *ok is false
+// when base + depth + 1 passes 2^64 - 1. Depth comes from the row table or
+// the row index (q35_sample.cu:180-181; spec 06 section 5).
+__device__ __forceinline__ uint64_t position_of(const SmpArgs& A, int row, int d, bool* ok) {
+  if (A.pos_mode == POS_BASE) {
+    const uint64_t depth = A.row_depth ? (uint64_t)A.row_depth[A.row0 + row] : (uint64_t)(A.row0 + row);
+    const uint64_t b = *A.base_position;
+    *ok = b <= ~0ull - (depth + 1u);
+    return b + depth + 1u;
+  }
+  *ok = true;
   return A.positions[(int64_t)row * A.n_draws + d];
+}
+__device__ __forceinline__ uint64_t position_of(const SmpArgs& A, int row, int d) {
+  bool ok;
+  return position_of(A, row, d, &ok);
 }
 
 // ---------------------------------------------------------------------------
@@ -608,18 +622,15 @@ __device__ __forceinline__ void sample_tail_wave(const SmpArgs& A, const DevPara
 // ---------------------------------------------------------------------------
 // Dense path: exact sorted order of every element with key >= theta_D.
 // ---------------------------------------------------------------------------
+// The exact need-th largest key of the row (1 <= need <= V): four 8-bit
+// radix passes from the top over the whole row. hist: 256 LDS words, bc: 2.
+// Block-wide; every thread returns the key.
 template <int DT, bool PEN>
-__device__ __forceinline__ int64_t dense_build(const SmpArgs& A, const RowCtx& rc, int row, uint32_t theta_rel,
-                               bool need_rel, int KB, uint32_t* lds, int* redi) {
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int V = A.V;
-  uint32_t* hist = lds;              // 256
-  uint32_t* dbase = lds + 256;       // 256
-  uint32_t* wcnt = lds + 512;        // NW * 256
-  uint32_t* bc = lds + 512 + NW * 256;  // broadcast words
-  // (a) exact KB-th largest key: four 8-bit radix passes from the top
+__device__ __forceinline__ uint32_t radix_kth_key(const RowCtx& rc, int V, int64_t need_in, uint32_t* hist,
+                                                  uint32_t* bc) {
+  const int tid = threadIdx.x;
   uint32_t prefix = 0, mask = 0;
-  int need = KB;
+  int64_t need = need_in;
   for (int pass = 0; pass < 4; ++pass) {
     const int shift = 24 - 8 * pass;
     for (int i = tid; i < 256; i += NT) hist[i] = 0;
@@ -630,9 +641,10 @@ __device__ __forceinline__ int64_t dense_build(const SmpArgs& A, const RowCtx& r
     }
     __syncthreads();
     if (tid == 0) {
-      int cum = 0, dsel = 0;
+      int64_t cum = 0;
+      int dsel = 0;
       for (int d = 255; d >= 0; --d) {
-        const int h = (int)hist[d];
+        const int64_t h = (int64_t)hist[d];
         if (cum + h >= need) {
           dsel = d;
           need -= cum;
@@ -646,9 +658,23 @@ __device__ __forceinline__ int64_t dense_build(const SmpArgs& A, const RowCtx& r
     __syncthreads();
     prefix |= bc[0] << shift;
     mask |= 255u << shift;
-    need = (int)bc[1];
+    need = (int64_t)bc[1];
     __syncthreads();
   }
+  return prefix;
+}
+
+template <int DT, bool PEN>
+__device__ __forceinline__ int64_t dense_build(const SmpArgs& A, const RowCtx& rc, int row, uint32_t theta_rel,
+                               bool need_rel, int KB, uint32_t* lds, int* redi) {
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int V = A.V;
+  uint32_t* hist = lds;              // 256
+  uint32_t* dbase = lds + 256;       // 256
+  uint32_t* wcnt = lds + 512;        // NW * 256
+  uint32_t* bc = lds + 512 + NW * 256;  // broadcast words
+  // (a) exact KB-th largest key
+  const uint32_t prefix = radix_kth_key<DT, PEN>(rc, V, KB, hist, bc);
   uint32_t theta = prefix;
   if (need_rel && theta_rel < theta) theta = theta_rel;
   if (theta < 1u) theta = 1u;
@@ -954,10 +980,12 @@ __device__ __forceinline__ void load_chunk(const RowCtx& rc, int32_t V, int nch,
 }
 
 // Raw bits of chunk c through 16-byte buffer loads, no guards: the caller
-// ensures the row is 16-byte aligned (so its length is a multiple of the
-// 16-byte groups). The resource spans exactly the row: groups of the last,
-// ragged chunk past its end are out of range and return zeros without
-// touching memory (chunk_values ignores them). The loads take a uniform
+// ensures the row starts 16-byte aligned and that every 16-byte group of the
+// chunk lies either wholly inside the row or wholly past its end (the
+// ragged last chunk comes here only when the row length is a whole number of
+// groups). The resource spans exactly the row: groups past its end are out
+// of range and return zeros without touching memory (chunk_values ignores
+// them). The loads take a uniform
 // chunk offset in an SGPR and loop-invariant lane offsets in VGPRs, so the
 // stream spends no vector instructions on addresses. With `live` false the
 // same loads go through a resource of size 0: every one is out of range. Issuing the same loads on every path, and keeping address
@@ -1283,6 +1311,7 @@ __global__ __launch_bounds__(NT) void smp_row(SmpArgs A) {
   __shared__ double s_mass[NW];
   __shared__ TailShared ts;
   __shared__ uint64_t s_pos;       // position of the row's first draw
+  __shared__ int32_t s_pos_ok;     // that position is representable
   __shared__ uint32_t s_rank[64];  // ranks of up to 64 final candidates
   __shared__ double s_wpre[64];    // their weights, in compaction order
   __shared__ double s_spre[64];    // their version-3 scores, in compaction order
@@ -1298,9 +1327,12 @@ __global__ __launch_bounds__(NT) void smp_row(SmpArgs A) {
   const int nch = (V + WSEG - 1) / WSEG;
   // Chunks [0, nfull) are read by the double-buffered stream with
   // range-checked buffer loads: every chunk of an aligned row, the ragged
-  // last one included. An unaligned row goes through the guarded path after
-  // it instead.
-  const int nfull = VEC ? nch : 0;
+  // last one included when the row is a whole number of 16-byte groups (a
+  // group straddling the row end would make one 16-byte load only partly in
+  // range: that chunk goes to the guarded loads after the stream, like every
+  // chunk of an unaligned row).
+  const bool whole_groups = ((uint32_t)V * (DT == 0 ? 4u : 2u)) % 16u == 0u;
+  const int nfull = VEC ? (whole_groups ? nch : V / WSEG) : 0;
   uint32_t buf0[EPT], buf1[EPT];
   load_full<DT>(row_base, V, wave, wave < nfull, lane, buf0);
   __builtin_amdgcn_sched_barrier(0);  // buf0's loads first: the stream waits for them first
@@ -1467,8 +1499,12 @@ __global__ __launch_bounds__(NT) void smp_row(SmpArgs A) {
   // (a uniform branch: a scalar load, which leaves the vector-memory
   // counter, and so the stream's waits, alone)
   if (wave == NW - 1 && A.out_ids != nullptr) {
-    const uint64_t p0 = position_of(A, row, 0);
-    if (lane == 0) s_pos = p0;
+    bool ok;
+    const uint64_t p0 = position_of(A, row, 0, &ok);
+    if (lane == 0) {
+      s_pos = p0;
+      s_pos_ok = ok ? 1 : 0;
+    }
   }
   // Chunks [0, nfull) are handed out as the waves free their buffers: wave w
   // starts with chunks w and w + NW (already requested) and then claims the
@@ -1587,6 +1623,7 @@ __global__ __launch_bounds__(NT) void smp_row(SmpArgs A) {
   int32_t status = ST_OK;
   if (rflags & F_INVALID) status = ST_EINVAL;
   else if (rflags & F_NONFINITE) status = ST_ENONFINITE;
+  else if (A.out_ids && !s_pos_ok) status = ST_EINVAL;  // prediction position overflow
 
   if (status == ST_OK) {
     // Every element with key >= theta_f = row_threshold(M, theta) was
@@ -1594,7 +1631,8 @@ __global__ __launch_bounds__(NT) void smp_row(SmpArgs A) {
     // or above theta_f are exactly the row's: sorted, they hold the top-KB
     // and every relevant element, which is all the outputs and the tail read.
     const uint32_t theta_f = row_threshold(plan, P, M, theta);
-    bool dense = A.force_dense != 0;
+    bool dense = A.force_dense != 0 || (P.zcheck && plan.sampled);
+    bool zfail = false;
     int64_t ncand = 0;
     bool sorted = false;
     // a single draw that the wave path takes: its weights and scores can be
@@ -1686,6 +1724,17 @@ __global__ __launch_bounds__(NT) void smp_row(SmpArgs A) {
       __syncthreads();
       cand = A.dense_a + (int64_t)row * A.dense_ld;
       wbuf = A.dense_w + (int64_t)row * A.dense_ld;
+      if (P.zcheck && plan.sampled) {
+        // The reference fails the row when any of its k candidates has a
+        // non-finite z = (l - l_0) / T (output_head_sampler.rs:146-153); z
+        // falls with l, so the k-th largest value decides.
+        uint32_t* lw = (uint32_t*)fl.cand;
+        const int64_t kk = plan.k_eff < (int64_t)V ? plan.k_eff : (int64_t)V;
+        const uint32_t kkey = radix_kth_key<DT, PEN>(rc, V, kk, lw, lw + 512 + NW * 256);
+        const double z = ((double)key2f(kkey) - (double)M) / P.temperature;
+        zfail = !(z - z == 0.0);
+        __syncthreads();
+      }
     }
 
     __syncthreads();  // the sorted candidates are visible to every thread
@@ -1756,8 +1805,12 @@ __global__ __launch_bounds__(NT) void smp_row(SmpArgs A) {
       if (A.nll_targets[row] >= (uint32_t)V) status = ST_EINVAL;
     }
     // ---- token selection ---------------------------------------------------
+    if (zfail) status = ST_ENONFINITE;
     if (A.out_ids) {
-      if (P.greedy) {
+      if (zfail) {
+        const int nd = A.mode == MODE_VERIFY ? 1 : A.n_draws;
+        for (int d = tid; d < nd; d += NT) A.out_ids[(int64_t)row * A.n_draws + d] = 0xffffffffu;
+      } else if (P.greedy) {
         const int nd = A.mode == MODE_VERIFY ? 1 : A.n_draws;
         for (int d = tid; d < nd; d += NT) A.out_ids[(int64_t)row * A.n_draws + d] = amax;
       } else if (ncand <= 64 && (A.mode == MODE_VERIFY || A.n_draws == 1)) {
@@ -1799,7 +1852,26 @@ __global__ __launch_bounds__(NT) void smp_row(SmpArgs A) {
     if (A.row_status) A.row_status[row] = status;
   }
 
+  // ---- single-row decode: advance the device position and token ---------
+  // (q35_sample.cu:206: *adv_pos += 1, *adv_tok = id). The host admits it
+  // for one row only; the row's position was read before this point, so the
+  // position counter may be the one the row was sampled at.
+  if (A.mode == MODE_SAMPLE && A.adv_pos) {
+    __syncthreads();
+    if (tid == 0 && status == ST_OK) {
+      const uint32_t tok = __hip_atomic_load(&A.out_ids[(int64_t)row * A.n_draws], __ATOMIC_RELAXED,
+                                             __HIP_MEMORY_SCOPE_AGENT);
+      *A.adv_pos += 1u;
+      *A.adv_tok = tok;
+    }
+  }
+
   // ---- verify: the last finished row applies the acceptance rule --------
+  // Rows are walked in order like speculation.rs:483-523: a failed row
+  // fails the pass only when the walk reaches it (rows after the first
+  // mismatch or EOS are never selected, :520-522). With a commit target the
+  // position advances by the tokens emitted and the token becomes the last
+  // of them, as Engine35::commit does on the host (engine35.cpp:1319-1329).
   if (A.mode == MODE_VERIFY) {
     __syncthreads();
     if (tid == 0) {
@@ -1809,25 +1881,37 @@ __global__ __launch_bounds__(NT) void smp_row(SmpArgs A) {
       if (old == (uint32_t)(A.rows - 1)) {
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
         uint32_t emitted = 0, accepted = 0, token = 0xffffffffu;
-        int32_t stop_eos = 0;
-        bool ok = true;
-        for (int j = 0; j < A.rows; ++j) ok = ok && (A.status[j] == ST_OK);
-        if (ok) {
-          for (int j = 0; j < A.rows; ++j) {
-            const uint32_t sel = A.out_ids[j];
-            ++emitted;
-            token = sel;
-            const bool matched = (j + 1 < A.rows) && A.drafts[j] == sel;
-            accepted += matched ? 1u : 0u;
-            for (int e = 0; e < A.n_eos; ++e)
-              if (A.eos[e] == sel) stop_eos = 1;
-            if (stop_eos || !matched) break;
+        int32_t stop_eos = 0, vstatus = ST_OK;
+        for (int j = 0; j < A.rows; ++j) {
+          const int32_t sj = A.status[j];
+          if (sj != ST_OK) {
+            vstatus = sj;
+            break;
           }
+          const uint32_t sel = A.out_ids[j];
+          ++emitted;
+          token = sel;
+          const bool matched = (j + 1 < A.rows) && A.drafts[j] == sel;
+          accepted += matched ? 1u : 0u;
+          for (int e = 0; e < A.n_eos; ++e)
+            if (A.eos[e] == sel) stop_eos = 1;
+          if (stop_eos || !matched) break;
         }
-        A.vresult[0] = accepted;
-        A.vresult[1] = emitted;
-        A.vresult[2] = token;
-        A.vresult[3] = (uint32_t)stop_eos;
+        if (vstatus != ST_OK) {
+          emitted = 0;
+          accepted = 0;
+          token = 0xffffffffu;
+          stop_eos = 0;
+        }
+        A.vresult[VR_ACCEPTED] = accepted;
+        A.vresult[VR_EMITTED] = emitted;
+        A.vresult[VR_TOKEN] = token;
+        A.vresult[VR_STOP_EOS] = (uint32_t)stop_eos;
+        A.vresult[VR_STATUS] = (uint32_t)vstatus;
+        if (vstatus == ST_OK && A.adv_pos) {
+          *A.adv_pos += emitted;
+          *A.adv_tok = token;
+        }
         __hip_atomic_store(A.vcount, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       }
     }
@@ -1851,7 +1935,7 @@ __global__ __launch_bounds__(1024) void smp_penalty_prep(PenArgs A) {
   uint32_t* bm = A.bitmap + (int64_t)row * A.bm_ld;
   const int words = (A.V + 31) >> 5;
   for (int i = tid; i < words; i += 1024) bm[i] = 0u;
-  if (tid == 0) s_bad = (len < 0 || len > HCAP) ? 1 : 0;
+  if (tid == 0) s_bad = (len < 0 || len > HCAP || (A.history_ld > 0 && (int64_t)len > A.history_ld)) ? 1 : 0;
   __syncthreads();
   if (s_bad) {
     if (tid == 0) A.len[row] = -1;

@@ -191,4 +191,60 @@ __device__ __forceinline__ double uniform_v2(uint64_t seed, uint64_t position) {
   return (double)(position_key(seed, position) >> 11) * (1.0 / 9007199254740992.0);
 }
 
+// Correctly rounded binary32 square root from an integer square root. The
+// reference fixes the result (portable_math.rs:61-106: round to nearest,
+// independent of a platform math library), not the method. A normalised
+// radicand m in [2^46, 2^48) with an even exponent has r = floor(sqrt(m)) of
+// 24 bits (or 2^24 after rounding up); m - r^2 > r decides round-to-nearest,
+// since m = (r + 1/2)^2 is impossible for an integer m.
+__host__ __device__ __forceinline__ float sqrt_rn_f32(float value) {
+  uint32_t b;
+  __builtin_memcpy(&b, &value, 4);
+  if ((b & 0x7fffffffu) == 0u || b == 0x7f800000u) return value;  // +-0, +inf
+  if ((b & 0x80000000u) || (b & 0x7f800000u) == 0x7f800000u) return __builtin_nanf("");
+  uint64_t sig;
+  int e;  // value = sig * 2^e
+  if ((b >> 23) == 0u) {
+    sig = b & 0x007fffffu;
+    e = -149;
+  } else {
+    sig = (uint64_t)((b & 0x007fffffu) | 0x00800000u);
+    e = (int)(b >> 23) - 150;
+  }
+  const int top = 63 - __builtin_clzll(sig);
+  int shift = 46 - top;
+  int ee = e - shift;
+  if (ee & 1) {
+    shift += 1;
+    ee -= 1;
+  }
+  uint64_t m = sig << shift;
+  // bit-by-bit integer square root
+  uint64_t r = 0, bit = 1ull << 46;
+  while (bit > m) bit >>= 2;
+  uint64_t rem = m;
+  while (bit) {
+    if (rem >= r + bit) {
+      rem -= r + bit;
+      r = (r >> 1) + bit;
+    } else {
+      r >>= 1;
+    }
+    bit >>= 2;
+  }
+  if (rem > r) r += 1;
+  int ex = ee / 2;
+  if (r == (1ull << 24)) {
+    r >>= 1;
+    ex += 1;
+  }
+  const uint32_t out = ((uint32_t)(ex + 23 + 127) << 23) | ((uint32_t)r & 0x007fffffu);
+  float f;
+  __builtin_memcpy(&f, &out, 4);
+  return f;
+}
+
+// 1 / sqrt_rn(value), the division separately rounded (portable_math.rs:108-111).
+__device__ __forceinline__ float rsqrt_rn_f32(float value) { return __fdiv_rn(1.0f, sqrt_rn_f32(value)); }
+
 }  // namespace yskn

@@ -319,7 +319,8 @@ inline Result<VerifyResult> verify_block(const SamplingParameters& params, bool 
   if (!ok) return Error{Error::Kind::Device, "hipMemcpy failed"};
   st = yskn_smp_verify(hd.value()->h, d_logits.p, YSKN_SMP_F32, (int32_t)rows, (int32_t)V, (int64_t)V,
                        (const uint32_t*)d_drafts.p, (const uint64_t*)d_pos.p, n_eos ? (const uint32_t*)d_eos.p : nullptr,
-                       (int32_t)n_eos, (uint32_t*)d_ids.p, (yskn_smp_verify_result*)d_res.p, nullptr);
+                       (int32_t)n_eos, (uint32_t*)d_ids.p, (yskn_smp_verify_result*)d_res.p, nullptr, nullptr,
+                       nullptr);
   if (st != YSKN_SMP_OK) return detail::from_status(st);
   st = yskn_smp_sync(hd.value()->h, nullptr);
   if (st != YSKN_SMP_OK) return detail::from_status(st);

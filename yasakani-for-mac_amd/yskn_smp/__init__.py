@@ -102,12 +102,16 @@ class CAux(C.Structure):
     ]
 
 
+class CAdvance(C.Structure):
+    _fields_ = [("position", C.c_void_p), ("token", C.c_void_p)]
+
+
 EXPORTED = [
     "yskn_smp_last_error", "yskn_smp_create", "yskn_smp_destroy", "yskn_smp_set_params",
     "yskn_smp_sample", "yskn_smp_argmax", "yskn_smp_top_tokens", "yskn_smp_nll",
     "yskn_smp_verify", "yskn_smp_sync", "yskn_smp_select_host", "yskn_smp_validate_params",
     "yskn_smp_version", "yskn_smp_get_stats", "yskn_smp_set_params_f64",
-    "yskn_smp_validate_params_f64",
+    "yskn_smp_validate_params_f64", "yskn_smp_sample_at", "yskn_smp_pm_test",
 ]
 
 _lib = None
@@ -132,7 +136,11 @@ def load_library(path: str = LIB_PATH) -> C.CDLL:
     L.yskn_smp_argmax.argtypes = [vp, vp, i32, i32, i32, i64, vp, vp]
     L.yskn_smp_top_tokens.argtypes = [vp, vp, i32, i32, i32, i64, i32, vp, vp, vp]
     L.yskn_smp_nll.argtypes = [vp, vp, i32, i32, i32, i64, vp, vp, vp]
-    L.yskn_smp_verify.argtypes = [vp, vp, i32, i32, i32, i64, vp, vp, vp, i32, vp, vp, vp]
+    L.yskn_smp_verify.argtypes = [vp, vp, i32, i32, i32, i64, vp, vp, vp, i32, vp, vp, C.POINTER(CAux),
+                                  C.POINTER(CAdvance), vp]
+    L.yskn_smp_sample_at.argtypes = [vp, vp, i32, i32, i32, i64, vp, vp, i32, vp, C.POINTER(CAux),
+                                     C.POINTER(CAdvance), vp]
+    L.yskn_smp_pm_test.argtypes = [i32, u64, vp, vp, i64]
     L.yskn_smp_sync.argtypes = [vp, vp]
     L.yskn_smp_select_host.argtypes = [vp, vp, i32, u64, C.POINTER(u32)]
     L.yskn_smp_validate_params.argtypes = [C.POINTER(CParams), i32, u32]
@@ -142,7 +150,8 @@ def load_library(path: str = LIB_PATH) -> C.CDLL:
     L.yskn_smp_get_stats.restype = C.c_int
     for name in ("yskn_smp_create", "yskn_smp_set_params", "yskn_smp_sample", "yskn_smp_argmax",
                  "yskn_smp_top_tokens", "yskn_smp_nll", "yskn_smp_verify", "yskn_smp_sync",
-                 "yskn_smp_select_host", "yskn_smp_validate_params"):
+                 "yskn_smp_select_host", "yskn_smp_validate_params", "yskn_smp_sample_at",
+                 "yskn_smp_pm_test"):
         L[name].restype = C.c_int
     _lib = L
     return L
@@ -297,19 +306,12 @@ class DeviceSampler:
             raise InvalidInput(EINVAL, "logits must be a 2-D CUDA tensor with unit column stride")
         return logits.shape[0], logits.shape[1], logits.stride(0)
 
-    def sample(self, logits, positions, *, argmax=False, top8=False, top20=False,
-               n_logprobs=0, history=None, history_len=None, row_status=False):
-        """Sample; positions is an int64 tensor [rows] or [rows, n_draws] of
-        absolute prediction positions. Returns a dict of device tensors."""
+    def _aux(self, rows, dev, out, argmax=False, top8=False, top20=False, n_logprobs=0,
+             history=None, history_len=None, row_status=False) -> CAux:
+        """Optional outputs (allocated into `out`) and the penalty history.
+        A 1-D history is shared by every row (history_ld = 0); a 2-D history
+        must have one row per logits row."""
         torch = self.torch
-        rows, V, ld = self._check_logits(logits)
-        pos = positions.to(torch.int64)
-        if pos.dim() == 1:
-            pos = pos.reshape(rows, 1)
-        pos = pos.contiguous()
-        n_draws = pos.shape[1]
-        dev = logits.device
-        out = {"ids": torch.empty((rows, n_draws), dtype=torch.int32, device=dev)}
         aux = CAux()
         if argmax:
             out["argmax"] = torch.empty(rows, dtype=torch.int32, device=dev)
@@ -333,17 +335,63 @@ class DeviceSampler:
         if history is not None:
             hist = history.to(torch.int32).contiguous()
             if hist.dim() == 1:
-                hist = hist.reshape(1, -1)
+                ld, width = 0, hist.shape[0]
+            elif hist.dim() == 2 and hist.shape[0] == rows:
+                ld, width = hist.stride(0), hist.shape[1]
+            else:
+                raise InvalidInput(EINVAL, "invalid input: history must be 1-D (shared) or have one row per logits row")
             hl = history_len
             if hl is None:
-                hl = torch.full((rows,), hist.shape[1], dtype=torch.int32, device=dev)
+                hl = torch.full((rows,), width, dtype=torch.int32, device=dev)
             hl = hl.to(torch.int32).contiguous()
+            if hl.numel() != rows:
+                raise InvalidInput(EINVAL, "invalid input: history_len needs one entry per row")
             out["_hist"], out["_hl"] = hist, hl
-            aux.history, aux.history_len, aux.history_ld = hist.data_ptr(), hl.data_ptr(), hist.stride(0)
+            aux.history, aux.history_len, aux.history_ld = hist.data_ptr(), hl.data_ptr(), ld
+        return aux
+
+    def sample(self, logits, positions, *, argmax=False, top8=False, top20=False,
+               n_logprobs=0, history=None, history_len=None, row_status=False):
+        """Sample; positions is an int64 tensor [rows] or [rows, n_draws] of
+        absolute prediction positions. Returns a dict of device tensors."""
+        torch = self.torch
+        rows, V, ld = self._check_logits(logits)
+        pos = positions.to(torch.int64)
+        if pos.dim() == 1:
+            pos = pos.reshape(rows, 1)
+        pos = pos.contiguous()
+        n_draws = pos.shape[1]
+        dev = logits.device
+        out = {"ids": torch.empty((rows, n_draws), dtype=torch.int32, device=dev)}
+        aux = self._aux(rows, dev, out, argmax, top8, top20, n_logprobs, history, history_len, row_status)
         out["_pos"] = pos
         _raise(self.L.yskn_smp_sample(self.h, logits.data_ptr(), self._dtype(logits), rows, V, ld,
                                       pos.data_ptr(), n_draws, out["ids"].data_ptr(),
                                       C.byref(aux), self._stream()))
+        return out
+
+    def sample_at(self, logits, base_position, *, row_depth=None, row0=0, advance=None,
+                  argmax=False, top8=False, top20=False, n_logprobs=0, history=None,
+                  history_len=None, row_status=False):
+        """Sample at device positions *base_position + depth + 1 (depth from
+        row_depth[row0 + r] or row0 + r). advance = (position int64 tensor [1],
+        token int32 tensor [1]) advances them on the device (one row only)."""
+        torch = self.torch
+        rows, V, ld = self._check_logits(logits)
+        dev = logits.device
+        out = {"ids": torch.empty(rows, dtype=torch.int32, device=dev)}
+        aux = self._aux(rows, dev, out, argmax, top8, top20, n_logprobs, history, history_len, row_status)
+        adv = None
+        if advance is not None:
+            adv = CAdvance(advance[0].data_ptr(), advance[1].data_ptr())
+        depth_ptr = None
+        if row_depth is not None:
+            out["_depth"] = row_depth.to(torch.uint8).contiguous()
+            depth_ptr = out["_depth"].data_ptr()
+        _raise(self.L.yskn_smp_sample_at(self.h, logits.data_ptr(), self._dtype(logits), rows, V, ld,
+                                         base_position.data_ptr(), depth_ptr, row0, out["ids"].data_ptr(),
+                                         C.byref(aux), C.byref(adv) if adv is not None else None,
+                                         self._stream()))
         return out
 
     def argmax(self, logits):
@@ -373,21 +421,31 @@ class DeviceSampler:
                                    t.data_ptr(), out.data_ptr(), self._stream()))
         return out
 
-    def verify(self, logits, drafts, base_position, eos_ids: Sequence[int] = ()):
-        """One-launch verification of M rows; returns (ids[M], result[4]) device
-        tensors: result = (accepted, emitted, token, stop_eos)."""
+    def verify(self, logits, drafts, base_position, eos_ids: Sequence[int] = (), *, commit=None,
+               argmax=False, top8=False, top20=False, n_logprobs=0, history=None,
+               history_len=None, row_status=False):
+        """One-launch verification of M rows; returns (ids[M], result[5], keep)
+        with result = (accepted, emitted, token, stop_eos, status) as device
+        int32 and `keep` holding the buffers (and the optional outputs, as a
+        dict, in keep[-1]). commit = (position int64 [1], token int32 [1])
+        advances them on the device when the pass succeeds."""
         torch = self.torch
         M, V, ld = self._check_logits(logits)
         dev = logits.device
         d = drafts.to(torch.int32).contiguous() if M > 1 else torch.zeros(1, dtype=torch.int32, device=dev)
-        bp = base_position.to(torch.int64).reshape(1).contiguous()
+        bp = base_position.to(torch.int64).reshape(1).contiguous() if base_position.dtype != torch.int64 \
+            else base_position.reshape(1)
         eos = torch.tensor(list(eos_ids) or [0], dtype=torch.int32, device=dev)
         ids = torch.empty(M, dtype=torch.int32, device=dev)
-        res = torch.empty(4, dtype=torch.int32, device=dev)
+        res = torch.empty(5, dtype=torch.int32, device=dev)
+        outs = {}
+        aux = self._aux(M, dev, outs, argmax, top8, top20, n_logprobs, history, history_len, row_status)
+        adv = CAdvance(commit[0].data_ptr(), commit[1].data_ptr()) if commit is not None else None
         _raise(self.L.yskn_smp_verify(self.h, logits.data_ptr(), self._dtype(logits), M, V, ld,
                                       d.data_ptr(), bp.data_ptr(), eos.data_ptr(), len(eos_ids),
-                                      ids.data_ptr(), res.data_ptr(), self._stream()))
-        return ids, res, (d, bp, eos)
+                                      ids.data_ptr(), res.data_ptr(), C.byref(aux),
+                                      C.byref(adv) if adv is not None else None, self._stream()))
+        return ids, res, (d, bp, eos, outs)
 
     def sync(self) -> None:
         _raise(self.L.yskn_smp_sync(self.h, self._stream()))
@@ -473,3 +531,23 @@ def negative_log_likelihood(logits, target: int) -> float:
 
 def version() -> str:
     return load_library().yskn_smp_version().decode()
+
+
+def pm_test(fn: int, inputs=None, base: int = 0, n: int = 0) -> np.ndarray:
+    """yskn_smp_pm_test: one device primitive on host inputs (see
+    include/yskn_smp.h). fn 10/11/14 take u64 words (binary64 bits or
+    integers), 12 takes (seed, position, token) rows, 13 (seed, position)
+    rows, 6/7 the binary32 bit patterns base .. base + n - 1."""
+    L = load_library()
+    if fn in (6, 7):
+        out = np.zeros(n, np.uint32)
+        _raise(L.yskn_smp_pm_test(fn, base, None, out.ctypes.data, n))
+        return out
+    a = np.ascontiguousarray(inputs)
+    if a.dtype == np.float64:
+        a = a.view(np.uint64)
+    a = np.ascontiguousarray(a, dtype=np.uint64)
+    n = a.shape[0]
+    out = np.zeros(n, np.uint64)
+    _raise(L.yskn_smp_pm_test(fn, 0, a.ctypes.data, out.ctypes.data, n))
+    return out
