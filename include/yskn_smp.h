@@ -204,6 +204,42 @@ int yskn_smp_sample_at(yskn_smp_handle h, const void* logits, int32_t dtype, int
                        const uint8_t* row_depth, int32_t row0, uint32_t* out_ids,
                        const yskn_smp_aux* aux, const yskn_smp_advance* advance, void* stream);
 
+/* The output head's epilogue fused into the sampler: instead of binary32
+ * logits the call reads the head's int64 accumulators and forms every logit
+ * while streaming, in the reference's exact order
+ *     inverse_rms = 1 / sqrt_rn(fold_add32(block_sums[row]) / width + epsilon)
+ *     logit[v]    = (((float)acc[row][v] * unit_scale[row]) * inverse_rms) * tau[v]
+ * (one round-to-nearest int64 -> binary32 conversion, each product separately
+ * rounded; spec 06 section 2, docs/spec/06_OUTPUT_HEAD_SAMPLER.md:31-55;
+ * src/misc_kernels.cu:57-73 with src/a8_prologue.cuh:10-15 argmax_stage1 /
+ * xsum_combine; crates/yskn-ref/src/compressed_linear.rs:329-340 and
+ * residual_norm_mlp.rs:37-46 with the portable rsqrt, portable_math.rs:61-111).
+ * A non-finite sum, argument, inverse RMS or logit fails the row with
+ * YSKN_SMP_ENONFINITE, as require_finite does there. */
+typedef struct yskn_smp_head {
+  const int64_t* acc;       /* device [rows x acc_ld] int64 accumulators */
+  int64_t acc_ld;           /* >= vocab */
+  const float* unit_scale;  /* device [rows] the common XSUM scale (row quantum) */
+  const float* block_sums;  /* device [rows x n_blocks] stored block sums of squares */
+  int32_t n_blocks;         /* 1..64 (10 for a width of 5,120) */
+  float width;              /* finite, > 0: the hidden width (5,120) */
+  float epsilon;            /* finite, > 0 */
+  const float* tau;         /* device [vocab] per-token weight scale */
+  float* logits_out;        /* optional device [rows x logits_ld]: the logits, written once */
+  int64_t logits_ld;        /* >= vocab when logits_out is set */
+  int32_t clear_acc;        /* 1: zero each accumulator once read, like xsum_combine
+                               (src/a8_prologue.cuh:10-12); needs logits_out */
+} yskn_smp_head;
+
+/* yskn_smp_sample on head accumulators (see yskn_smp_head): the same
+ * positions, draws, outputs and errors, with the logits formed in the
+ * sampler's own sweep instead of being written and read again by a separate
+ * epilogue launch (the reference's argmax_stage1 -> smp2_kernel pair,
+ * src/engine35.cpp:810-821). */
+int yskn_smp_sample_head(yskn_smp_handle h, const yskn_smp_head* head, int32_t rows, int32_t vocab,
+                         const uint64_t* positions, int32_t n_draws, uint32_t* out_ids,
+                         const yskn_smp_aux* aux, void* stream);
+
 /* Greedy argmax per row: greedy() (output_head_sampler.rs:103-113),
  * launch_argmax (src/args.hpp:24-30; src/misc_kernels.cu:57-96).
  * Like the two entry points below, a pure function of the logits: the

@@ -23,7 +23,7 @@ import pytest
 import torch
 
 import yskn_oracle as O
-from gpu_helpers import oracle_params, oracle_select, pmap, to_u32
+from gpu_helpers import assert_logprobs_close, oracle_params, oracle_select, pmap, to_u32
 
 pytestmark = pytest.mark.gpu
 
@@ -148,9 +148,13 @@ def test_padded_rows_with_a_ragged_last_group(dtype, V, ld):
     d = DeviceSampler(rows, V)
     sp = SamplingParameters(temperature_milli=800, top_p_milli=950, top_k=20, seed=V)
     d.set_params(sp)
-    out = d.sample(view, torch.arange(rows, device=DEV) + 3, argmax=True, top20=True)
+    out = d.sample(view, torch.arange(rows, device=DEV) + 3, argmax=True, top20=True, n_logprobs=20)
     d.sync()
     assert list(to_u32(out["argmax"])) == [O.greedy(xs[r]) for r in range(rows)]
+    for r in range(rows):
+        ids, lp = O.top_logprobs(xs[r], 20)
+        assert list(to_u32(out["logprob_ids"])[r]) == list(ids)
+        assert_logprobs_close(out["logprobs"][r].cpu().numpy(), lp)
     for r in range(rows):
         tt = O.top_tokens(xs[r], 20)
         assert list(to_u32(out["top20_ids"])[r]) == list(tt)

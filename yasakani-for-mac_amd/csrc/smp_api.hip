@@ -55,6 +55,9 @@ struct yskn_smp {
   uint32_t* d_pen_cnt = nullptr;
   int32_t* d_pen_len = nullptr;
   unsigned long long* d_stats = nullptr;
+  uint64_t* d_exp_cand = nullptr;  // [max_rows][SEG_MAX][EXP_CAP]
+  SegMeta* d_exp_meta = nullptr;   // [max_rows][SEG_MAX]
+  uint32_t* d_segcnt = nullptr;    // [max_rows]
   // host-slice convenience buffers
   float* d_host_logits = nullptr;
   uint64_t* d_host_pos = nullptr;
@@ -212,6 +215,31 @@ bool any_penalty(yskn_smp_handle h, int32_t rows) {
   return false;
 }
 
+// Segments per row. A block streams one segment; small batches split rows so
+// that the call spreads over the CUs (about one 2,048-logit chunk per wave,
+// about 512 blocks in all); from 192 rows on, each row is one block.
+// YSKN_SMP_SEGMENTS=n (1..32) fixes the count for measurements.
+int segments_for(int32_t rows, int32_t vocab) {
+  static const int forced = [] {
+    const char* e = std::getenv("YSKN_SMP_SEGMENTS");
+    return e ? std::atoi(e) : 0;
+  }();
+  const int nch = (vocab + WSEG - 1) / WSEG;
+  int s;
+  if (forced > 0) {
+    s = forced;
+  } else if (rows >= 192) {
+    s = 1;
+  } else {
+    const int by_chunks = (nch + NW - 1) / NW;
+    const int by_blocks = (512 + rows - 1) / rows;
+    s = by_chunks < by_blocks ? by_chunks : by_blocks;
+  }
+  if (s > SEG_MAX) s = SEG_MAX;
+  if (s > nch) s = nch;
+  return s < 1 ? 1 : s;
+}
+
 SmpArgs base_args(yskn_smp_handle h, const void* logits, int32_t rows, int32_t vocab,
                   int64_t ld) {
   SmpArgs a;
@@ -237,6 +265,10 @@ SmpArgs base_args(yskn_smp_handle h, const void* logits, int32_t rows, int32_t v
   a.dense_ld = h->dense_ld;
   a.force_dense = (h->flags & YSKN_SMP_FLAG_FORCE_DENSE) ? 1 : 0;
   a.stats = h->d_stats;
+  a.nseg = segments_for(rows, vocab);
+  a.exp_cand = h->d_exp_cand;
+  a.exp_meta = h->d_exp_meta;
+  a.segcnt = h->d_segcnt;
   return a;
 }
 
@@ -265,8 +297,8 @@ int launch(yskn_smp_handle h, SmpArgs& a, int32_t dtype, bool pen, const yskn_sm
     hipError_t e = launch_penalty_prep(p, st);
     if (e != hipSuccess) return hip_fail(e, "penalty preparation launch");
   }
-  a.vec = vector_ok(a.logits, dtype, a.ld) ? 1 : 0;
-  hipError_t e = launch_sample(a, dtype == YSKN_SMP_F32 ? 0 : 1, a.vec != 0, pen, st);
+  a.vec = dtype != 2 && vector_ok(a.logits, dtype, a.ld) ? 1 : 0;
+  hipError_t e = launch_sample(a, dtype == 2 ? 2 : (dtype == YSKN_SMP_F32 ? 0 : 1), a.vec != 0, pen, st);
   if (e != hipSuccess) return hip_fail(e, "sampler launch");
   h->last_rows = a.rows;
   h->last_verify = a.mode == MODE_VERIFY ? (const yskn_smp_verify_result*)a.vresult : nullptr;
@@ -359,6 +391,9 @@ int yskn_smp_create(int32_t max_rows, int32_t max_vocab, uint32_t flags, yskn_sm
   step(alloc(&h->d_pen_cnt, R * (size_t)HCAP));
   step(alloc(&h->d_pen_len, R));
   step(alloc(&h->d_stats, (size_t)STAT_COUNT));
+  step(alloc(&h->d_exp_cand, R * SEG_MAX * EXP_CAP));
+  step(alloc(&h->d_exp_meta, R * SEG_MAX));
+  step(alloc(&h->d_segcnt, R));
   step(alloc(&h->d_host_logits, (size_t)max_vocab));
   step(alloc(&h->d_host_pos, 1));
   step(alloc(&h->d_host_out, 1));
@@ -366,6 +401,7 @@ int yskn_smp_create(int32_t max_rows, int32_t max_vocab, uint32_t flags, yskn_sm
   if (e == hipSuccess) step(hipMemset(h->d_vcount, 0, 4 * sizeof(uint32_t)));
   if (e == hipSuccess) step(hipMemset(h->d_pen_len, 0, R * sizeof(int32_t)));
   if (e == hipSuccess) step(hipMemset(h->d_stats, 0, STAT_COUNT * sizeof(unsigned long long)));
+  if (e == hipSuccess) step(hipMemset(h->d_segcnt, 0, R * sizeof(uint32_t)));
   if (e == hipSuccess) {
     step(hipMemcpy(h->d_params, h->params.data(), sizeof(DevParams), hipMemcpyHostToDevice));
   }
@@ -383,7 +419,8 @@ void yskn_smp_destroy(yskn_smp_handle h) {
                   h->d_status,     h->d_vcount,    h->d_vresult,     h->d_dense_a,
                   h->d_dense_b,    h->d_dense_w,   h->d_pen_bitmap,  h->d_pen_ids,
                   h->d_pen_cnt,    h->d_pen_len,   h->d_stats,       h->d_host_logits,
-                  h->d_host_pos,   h->d_host_out};
+                  h->d_host_pos,   h->d_host_out,  h->d_exp_cand,    h->d_exp_meta,
+                  h->d_segcnt};
   for (void* p : ptrs)
     if (p) (void)hipFree(p);
   delete h;
@@ -477,6 +514,49 @@ int yskn_smp_sample_at(yskn_smp_handle h, const void* logits, int32_t dtype, int
   st = apply_aux(h, a, aux, rows, &pen);
   if (st) return st;
   return launch(h, a, dtype, pen, aux, (hipStream_t)stream);
+}
+
+int yskn_smp_sample_head(yskn_smp_handle h, const yskn_smp_head* head, int32_t rows, int32_t vocab,
+                         const uint64_t* positions, int32_t n_draws, uint32_t* out_ids,
+                         const yskn_smp_aux* aux, void* stream) {
+  if (!head) return fail(YSKN_SMP_EINVAL, "invalid input: null head");
+  int st = check_common(h, head->acc, YSKN_SMP_F32, rows, vocab, head->acc_ld);
+  if (st) return st;
+  if (!head->unit_scale || !head->block_sums || !head->tau)
+    return fail(YSKN_SMP_EINVAL, "invalid input: head needs unit_scale, block_sums and tau");
+  if (head->n_blocks < 1 || head->n_blocks > 64)
+    return fail(YSKN_SMP_EINVAL, "invalid input: head n_blocks must be in 1..=64");
+  if (!finite_f(head->width) || !(head->width > 0.0f))
+    return fail(YSKN_SMP_EINVAL, "invalid input: head width must be finite and positive");
+  if (!finite_f(head->epsilon) || !(head->epsilon > 0.0f))
+    return fail(YSKN_SMP_EINVAL, "invalid model: epsilon must be finite and positive");
+  if (head->logits_out && head->logits_ld < vocab)
+    return fail(YSKN_SMP_EINVAL, "invalid input: head logits_ld < vocab");
+  if (head->clear_acc && !head->logits_out)
+    return fail(YSKN_SMP_EINVAL, "invalid input: clearing the accumulators needs logits_out");
+  if (!h->params_shared && rows > (int32_t)h->params.size())
+    return fail(YSKN_SMP_EINVAL, "invalid input: fewer per-row parameter sets than rows");
+  if (out_ids && (!positions || n_draws < 1))
+    return fail(YSKN_SMP_EINVAL, "invalid input: out_ids needs positions and n_draws >= 1");
+  st = check_params_for(h, rows, vocab);
+  if (st) return st;
+  SmpArgs a = base_args(h, head->acc, rows, vocab, head->acc_ld);
+  a.positions = positions;
+  a.n_draws = n_draws < 1 ? 1 : n_draws;
+  a.out_ids = out_ids;
+  a.head_tau = head->tau;
+  a.head_us = head->unit_scale;
+  a.head_sums = head->block_sums;
+  a.head_nblk = head->n_blocks;
+  a.head_width = head->width;
+  a.head_eps = head->epsilon;
+  a.head_out = head->logits_out;
+  a.head_out_ld = head->logits_ld;
+  a.head_clear = head->clear_acc ? 1 : 0;
+  bool pen = false;
+  st = apply_aux(h, a, aux, rows, &pen);
+  if (st) return st;
+  return launch(h, a, 2, pen, aux, (hipStream_t)stream);
 }
 
 int yskn_smp_argmax(yskn_smp_handle h, const void* logits, int32_t dtype, int32_t rows,

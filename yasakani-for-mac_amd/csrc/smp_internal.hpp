@@ -18,6 +18,12 @@ constexpr int BUFCAP = 8192;       // candidates a row block's append buffer hol
 constexpr int DLANES = 16;         // lanes with survivors above which a chunk is deferred
 constexpr int DEFCAP = 1024;       // deferred chunks a row block records
 constexpr int KBMAX = 64;          // largest "small" top-k / list length
+// Segments: a row split over several blocks exports, per segment, every
+// candidate at or above the segment's own certified threshold (at most
+// EXP_CAP of them; more send the row to the dense path) for the row's last
+// block to finish. SEG_MAX * EXP_CAP fits the append buffer.
+constexpr int SEG_MAX = 32;
+constexpr int EXP_CAP = 256;
 constexpr int HCAP = 16384;        // history tokens per row for the penalties
 constexpr int64_t VMAX = 4194304;  // largest vocabulary
 
@@ -55,6 +61,17 @@ struct DevParams {
   int32_t zcheck;
 };
 
+// What a segment hands to the block that finishes its row.
+struct SegMeta {
+  uint32_t count;     // candidates exported (> EXP_CAP: overflow, none kept)
+  uint32_t flags;     // F_* seen in the segment
+  uint32_t mkey;      // the segment's largest key (0: none finite)
+  uint32_t pad;
+  double mass;        // sum of exp(l - mref) over the segment's mass terms
+  float mref;         // reference point of that mass (-inf: no terms)
+  float pad2;
+};
+
 // Counters for profiling the path (cumulative since create).
 enum StatIndex {
   STAT_ROWS = 0,      // rows finished
@@ -84,6 +101,22 @@ struct SmpArgs {
   const DevParams* prm;
   int32_t prm_shared;
   int32_t n_draws;
+  int32_t nseg;                  // segments (blocks) per row, 1..SEG_MAX
+  uint64_t* exp_cand;            // [rows][nseg][EXP_CAP] exported candidates
+  SegMeta* exp_meta;             // [rows][nseg]
+  uint32_t* segcnt;              // [rows] arrivals of the row's segments (left at 0)
+  // Head accumulators as the input (element type 2; spec 06 section 2): the
+  // logits are ((float)acc * unit_scale) * inverse_rms * tau, formed while
+  // streaming. `logits` then points at the int64 accumulators, `ld` is their
+  // row stride in elements.
+  const float* head_tau;         // [V]
+  const float* head_us;          // [rows] common XSUM scale
+  const float* head_sums;        // [rows][head_nblk] stored block sums of squares
+  int32_t head_nblk;
+  float head_width, head_eps;
+  float* head_out;               // optional [rows][head_out_ld] logits written out
+  int64_t head_out_ld;
+  int32_t head_clear;            // zero the accumulators once read (needs head_out)
   int32_t pos_mode;              // PosMode
   const uint64_t* positions;     // [rows * n_draws] (POS_ARRAY)
   const uint64_t* base_position; // POS_BASE: row r at *base + depth(r) + 1

@@ -312,6 +312,13 @@ __device__ int block_excl_scan(int cnt, int* red, int* total) {
 // ---------------------------------------------------------------------------
 struct RowCtx {
   const char* base;        // row start
+  // element type 2 (head accumulators)
+  const int64_t* acc;      // the row's accumulators
+  int64_t* accw;           // the same, to clear (or NULL)
+  const float* tau;        // [V]
+  float us, r;             // common scale, inverse RMS of the row
+  const float* lout;       // the row's logits written out (re-reads), or NULL
+  float* loutw;            // the same, to write (or NULL)
   const uint32_t* bitmap;  // penalty bitmap of the row (or NULL)
   const uint32_t* pids;
   const uint32_t* pcnt;
@@ -338,10 +345,24 @@ __device__ __forceinline__ uint32_t penalize(uint32_t bits, uint32_t c, const Ro
   return __float_as_uint(l);
 }
 
+// Head logit i from its int64 accumulator in the reference's exact order:
+// one round-to-nearest int64 -> binary32 conversion, then three separately
+// rounded binary32 multiplies (compressed_linear.rs:329-340; spec 06 section
+// 2; src/misc_kernels.cu:63-69).
+__device__ __forceinline__ float head_value(const RowCtx& r, int64_t i) {
+  float x = (float)r.acc[i];
+  x = __fmul_rn(x, r.us);
+  x = __fmul_rn(x, r.r);
+  return __fmul_rn(x, r.tau[i]);
+}
+
 template <int DT>
 __device__ __forceinline__ uint32_t raw_bits(const RowCtx& r, int64_t i) {
   if (DT == 0) return ((const uint32_t*)r.base)[i];
-  return (uint32_t)((const uint16_t*)r.base)[i] << 16;
+  if (DT == 1) return (uint32_t)((const uint16_t*)r.base)[i] << 16;
+  // a head row re-read: the logits written out, or formed again
+  if (r.lout) return __float_as_uint(r.lout[i]);
+  return __float_as_uint(head_value(r, i));
 }
 
 template <int DT, bool PEN>
@@ -763,6 +784,35 @@ __device__ __forceinline__ RowCtx make_rowctx(const SmpArgs& A, const DevParams&
                                               int dtype_bytes, uint32_t* flags) {
   RowCtx rc;
   rc.base = (const char*)A.logits + (int64_t)row * A.ld * dtype_bytes;
+  rc.acc = nullptr;
+  rc.accw = nullptr;
+  rc.tau = nullptr;
+  rc.us = 0.0f;
+  rc.r = 0.0f;
+  rc.lout = nullptr;
+  rc.loutw = nullptr;
+  if (A.head_tau) {
+    // inverse RMS of the row: the stored block sums folded from +0, divided
+    // by the width, plus epsilon, then 1 / sqrt_rn (residual_norm_mlp.rs:
+    // 37-46; portable_math.rs:108-111); every stage must stay finite
+    const float* S = A.head_sums + (int64_t)row * A.head_nblk;
+    float tot = 0.0f;
+    for (int b = 0; b < A.head_nblk; ++b) tot = __fadd_rn(tot, S[b]);
+    const float arg = __fadd_rn(__fdiv_rn(tot, A.head_width), A.head_eps);
+    const float r = rsqrt_rn_f32(arg);
+    if (nonfinite_bits(__float_as_uint(tot)) || nonfinite_bits(__float_as_uint(arg)) ||
+        nonfinite_bits(__float_as_uint(r)))
+      *flags |= F_NONFINITE;
+    rc.acc = (const int64_t*)rc.base;
+    if (A.head_clear) rc.accw = (int64_t*)rc.base;
+    rc.tau = A.head_tau;
+    rc.us = A.head_us[row];
+    rc.r = r;
+    if (A.head_out) {
+      rc.loutw = A.head_out + (int64_t)row * A.head_out_ld;
+      rc.lout = rc.loutw;
+    }
+  }
   rc.bitmap = nullptr;
   rc.pids = nullptr;
   rc.pcnt = nullptr;
@@ -922,6 +972,65 @@ __device__ void sort_desc_small(uint64_t* a, uint64_t* b, int n) {
   __syncthreads();
 }
 
+// The k-th largest key (1 <= k <= n) among n packed entries in LDS: four
+// 8-bit radix passes from the top; wave 0 finds each pass's digit from
+// suffix sums over the 256-bin histogram (four bins per lane). hist: 256
+// LDS words, bc: 2 more. Block-wide; every thread returns the key.
+__device__ uint32_t lds_kth_key(const uint64_t* buf, uint32_t n, uint32_t k, uint32_t* hist, uint32_t* bc) {
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  uint32_t prefix = 0u, mask = 0u, need = k;
+  for (int pass = 0; pass < 4; ++pass) {
+    const int shift = 24 - 8 * pass;
+    for (int i = tid; i < 256; i += NT) hist[i] = 0u;
+    __syncthreads();
+    for (uint32_t i = (uint32_t)tid; i < n; i += NT) {
+      const uint32_t kk = pk_key(buf[i]);
+      if ((kk & mask) == prefix) atomicAdd(&hist[(kk >> shift) & 255u], 1u);
+    }
+    __syncthreads();
+    if (wave == 0) {
+      uint32_t h[4], own = 0u;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        h[q] = hist[4 * lane + q];
+        own += h[q];
+      }
+      // suffix sum: entries in the bins of this lane and every higher lane
+      uint32_t suf = own;
+#pragma unroll
+      for (int o = 1; o < 64; o <<= 1) {
+        const uint32_t t = __shfl_down(suf, o);
+        if (lane + o < 64) suf += t;
+      }
+      const uint64_t reach = __ballot(suf >= need);
+      const int L = reach ? 63 - __builtin_clzll(reach) : -1;  // the highest lane still holding the k-th
+      if (L < 0 && lane == 0) {
+        bc[0] = 0u;  // fewer than k entries (the caller does not ask for that)
+        bc[1] = 1u;
+      }
+      if (lane == L) {
+        uint32_t cum = suf - own;                 // entries in higher lanes' bins
+        int dsel = 4 * L;
+        for (int q = 3; q >= 0; --q) {
+          if (cum + h[q] >= need) {
+            dsel = 4 * L + q;
+            break;
+          }
+          cum += h[q];
+        }
+        bc[0] = (uint32_t)dsel;
+        bc[1] = need - cum;
+      }
+    }
+    __syncthreads();
+    prefix |= bc[0] << shift;
+    mask |= 255u << shift;
+    need = bc[1];
+    __syncthreads();
+  }
+  return prefix;
+}
+
 // ---------------------------------------------------------------------------
 // LDS of a row block (136 KB in all with the small arrays: one block per CU).
 // ---------------------------------------------------------------------------
@@ -935,14 +1044,41 @@ struct RowLds {
 
 // Raw bits of chunk c (2,048 logits) of a row into kb; nothing for c >= nch.
 // Element (q, j) of this lane is eb + q * 64 * GRP + j.
+// For element type 2, `first` marks the chunk's first read: the head logits
+// are formed from the accumulators, written out and the accumulators
+// cleared when asked; later reads use the written logits (raw_bits).
 template <int DT, bool VEC>
 __device__ __forceinline__ void load_chunk(const RowCtx& rc, int32_t V, int nch, int c, int lane,
-                                           uint32_t (&kb)[EPT]) {
-  constexpr int GRP = (DT == 0) ? 4 : 8;
+                                           uint32_t (&kb)[EPT], bool first = true) {
+  constexpr int GRP = (DT == 1) ? 8 : 4;
   constexpr int NGRP = EPT / GRP;
   if (c >= nch) return;
   const uint32_t w0 = (uint32_t)c * WSEG;
   const uint32_t eb = w0 + (uint32_t)lane * GRP;
+  if (DT == 2) {
+    const int32_t lim = V - (int32_t)eb;
+#pragma unroll
+    for (int q = 0; q < NGRP; ++q) {
+#pragma unroll
+      for (int j = 0; j < GRP; ++j) {
+        const int32_t o = q * 64 * GRP + j;
+        uint32_t b = 0u;
+        if (o < lim) {
+          const int64_t i = (int64_t)eb + o;
+          if (first) {
+            const float f = head_value(rc, i);
+            if (rc.loutw) rc.loutw[i] = f;
+            if (rc.accw) rc.accw[i] = 0;
+            b = __float_as_uint(f);
+          } else {
+            b = raw_bits<DT>(rc, i);
+          }
+        }
+        kb[q * GRP + j] = b;
+      }
+    }
+    return;
+  }
   if (VEC && w0 + WSEG <= (uint32_t)V) {
     const uint4* src = (const uint4*)(rc.base + (size_t)eb * (DT == 0 ? 4 : 2));
 #pragma unroll
@@ -994,6 +1130,7 @@ __device__ __forceinline__ void load_chunk(const RowCtx& rc, int32_t V, int nch,
 template <int DT>
 __device__ __forceinline__ void load_full(const char* row_base, int32_t V, int c, bool live, int lane,
                                           uint32_t (&kb)[EPT]) {
+  if (DT == 2) return;  // head rows are not streamed through buffer loads
   constexpr int GRP = (DT == 0) ? 4 : 8;
   constexpr int NGRP = EPT / GRP;
   const __amdgpu_buffer_rsrc_t rs =
@@ -1026,7 +1163,7 @@ __device__ __forceinline__ void load_full(const char* row_base, int32_t V, int c
 template <int DT, bool PEN>
 __device__ __forceinline__ void chunk_values(const RowCtx& rc, int32_t V, int c, int lane,
                                              uint32_t (&kb)[EPT], float& lmax, bool& bad) {
-  constexpr int GRP = (DT == 0) ? 4 : 8;
+  constexpr int GRP = (DT == 1) ? 8 : 4;
   constexpr int NGRP = EPT / GRP;
   const uint32_t w0 = (uint32_t)c * WSEG;
   const uint32_t eb = w0 + (uint32_t)lane * GRP;
@@ -1169,7 +1306,7 @@ template <int DT>
 __device__ __forceinline__ void chunk_filter(int c, int lane, const uint32_t (&kb)[EPT], uint32_t thr,
                                              uint32_t mk, bool mass, uint32_t lk, uint32_t cmax, int defer_lanes,
                                              WaveState& ws, RowShared& sh, RowLds& fl, uint64_t* spill) {
-  constexpr int GRP = (DT == 0) ? 4 : 8;
+  constexpr int GRP = (DT == 1) ? 8 : 4;
   constexpr int NGRP = EPT / GRP;
   if (mk == 0u) return;  // nothing finite seen yet: the row is rejected anyway
   const float thf = key_threshold_float(thr);
@@ -1307,8 +1444,9 @@ __global__ __launch_bounds__(NT) void smp_row(SmpArgs A) {
   __shared__ uint64_t red_u64[NW];
   __shared__ double red_f64[NW];
   __shared__ int red_int[NW];
-  __shared__ float s_mref[NW];
-  __shared__ double s_mass[NW];
+  __shared__ float s_mref[SEG_MAX];   // mass terms: one per wave, or one per segment
+  __shared__ double s_mass[SEG_MAX];
+  __shared__ int32_t s_last;          // this block finishes the row
   __shared__ TailShared ts;
   __shared__ uint64_t s_pos;       // position of the row's first draw
   __shared__ int32_t s_pos_ok;     // that position is representable
@@ -1318,40 +1456,50 @@ __global__ __launch_bounds__(NT) void smp_row(SmpArgs A) {
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int row = blockIdx.x;
+  // A row is split into nseg segments of whole chunks, one block each; with
+  // nseg = 1 the block streams the whole row and finishes it directly.
+  const int nseg = A.nseg;
+  const int row = (int)blockIdx.x / nseg;
+  const int seg = (int)blockIdx.x - row * nseg;
   const int32_t V = A.V;
   // The wave's first two chunks are requested before anything else: they
   // need only the row's address, while the parameters take dependent scalar
   // loads (microseconds at the start of a launch).
-  const char* const row_base = (const char*)A.logits + (int64_t)row * A.ld * (DT == 0 ? 4 : 2);
+  constexpr int ES = DT == 0 ? 4 : (DT == 1 ? 2 : 8);  // bytes per input element
+  const char* const row_base = (const char*)A.logits + (int64_t)row * A.ld * ES;
   const int nch = (V + WSEG - 1) / WSEG;
-  // Chunks [0, nfull) are read by the double-buffered stream with
+  const int cb = (int)(((int64_t)seg * nch) / nseg);       // this block's chunks [cb, ce)
+  const int ce = (int)(((int64_t)(seg + 1) * nch) / nseg);
+  // Chunks [cb, sfull) are read by the double-buffered stream with
   // range-checked buffer loads: every chunk of an aligned row, the ragged
   // last one included when the row is a whole number of 16-byte groups (a
   // group straddling the row end would make one 16-byte load only partly in
   // range: that chunk goes to the guarded loads after the stream, like every
   // chunk of an unaligned row).
-  const bool whole_groups = ((uint32_t)V * (DT == 0 ? 4u : 2u)) % 16u == 0u;
+  const bool whole_groups = ((uint32_t)V * (uint32_t)ES) % 16u == 0u;
   const int nfull = VEC ? (whole_groups ? nch : V / WSEG) : 0;
+  const int sfull = nfull < ce ? nfull : ce;
   uint32_t buf0[EPT], buf1[EPT];
-  load_full<DT>(row_base, V, wave, wave < nfull, lane, buf0);
+  load_full<DT>(row_base, V, cb + wave, cb + wave < sfull, lane, buf0);
   __builtin_amdgcn_sched_barrier(0);  // buf0's loads first: the stream waits for them first
-  load_full<DT>(row_base, V, wave + NW, wave + NW < nfull, lane, buf1);
+  load_full<DT>(row_base, V, cb + wave + NW, cb + wave + NW < sfull, lane, buf1);
   __builtin_amdgcn_sched_barrier(0);  // both chunks in flight before any other work
   const DevParams P = A.prm[A.prm_shared ? 0 : row];
   const RowPlan plan = make_plan(A, P);
   uint32_t wflags = 0;
-  const RowCtx rc = make_rowctx<PEN>(A, P, row, DT == 0 ? 4 : 2, &wflags);
+  const RowCtx rc = make_rowctx<PEN>(A, P, row, ES, &wflags);
   if (tid == 0) {
     sh.count = 0u;
     sh.flags = 0u;
     sh.ndef = 0u;
-    sh.next = 2u * NW;  // chunks 0 .. 2 NW - 1 are the waves' first two
+    sh.next = (uint32_t)cb + 2u * NW;  // chunks cb .. cb + 2 NW - 1 are the waves' first two
   }
   if (tid < BW_N) sh.bw[tid] = 0u;
   if (tid < 64) s_rank[tid] = 0u;
   if (tid == 64) sh.ctr = 0u;
-  uint64_t* const spill = A.dense_b + (int64_t)row * A.dense_ld;
+  // each segment appends past BUFCAP into its own share of the row's spill area
+  const int64_t spill_share = A.dense_ld / nseg;
+  uint64_t* const spill = A.dense_b + (int64_t)row * A.dense_ld + (int64_t)seg * spill_share;
 
   WaveState ws;
   ws.wkey = 0u;
@@ -1360,7 +1508,7 @@ __global__ __launch_bounds__(NT) void smp_row(SmpArgs A) {
   ws.bad = false;
   ws.ab_cur = 0u;
   ws.ab_end = 0u;
-  ws.spill_cap = (uint32_t)A.dense_ld;
+  ws.spill_cap = (uint32_t)spill_share;
   __syncthreads();  // shared state initialised
 
   // Each wave keeps the KB largest lane maxima of its chunks so far, sorted
@@ -1384,8 +1532,11 @@ __global__ __launch_bounds__(NT) void smp_row(SmpArgs A) {
   // the final one comes from the union of their lists. (On 256 x 248,320
   // logits with KB = 20, inserting the first chunk's top KB at once cost
   // about 4 us per launch, eight per later chunk about 0.5 us.)
-  const int r_first = plan.KB < 2 ? plan.KB : 2;
-  const int r_next = r_first;
+  // A segmented row gives each wave about one chunk: its first chunk then
+  // inserts all its KB largest lane maxima, so that a certified bound exists
+  // at once (otherwise the segment would export every element).
+  const int r_next = plan.KB < 2 ? plan.KB : 2;
+  const int r_first = nseg > 1 ? plan.KB : r_next;
 
   // Below lo_f nothing can matter to this wave: no lane maximum would enter
   // its list (lo_f <= its KB-th value), no value would be a candidate
@@ -1397,11 +1548,12 @@ __global__ __launch_bounds__(NT) void smp_row(SmpArgs A) {
   // One chunk: c from X. In the stream, the wave claims its next chunk and
   // prefetches it into X (the claim is an LDS atomic issued first, its
   // result read last, so that its latency is hidden); returns that chunk.
-  auto step = [&](uint32_t (&X)[EPT], int c, bool first, bool stream) -> int {
+  // `live`: X holds chunk c (false for a buffer whose claim fell past the
+  // streamed chunks: nothing was loaded into it).
+  auto step = [&](uint32_t (&X)[EPT], int c, bool first, bool stream, bool live) -> int {
     uint32_t ticket = 0u;
     if (stream && lane == 0) ticket = atomicAdd(&sh.next, 1u);
     float lmax = -__builtin_inff();
-    const bool live = c < nch;
     if (live) chunk_values<DT, PEN>(rc, V, c, lane, X, lmax, ws.bad);
     if (live && (first || __ballot(lmax >= lo_f))) {
       const uint32_t lk = lmax == -__builtin_inff() ? 0u : f2key(__float_as_uint(lmax));
@@ -1486,10 +1638,10 @@ __global__ __launch_bounds__(NT) void smp_row(SmpArgs A) {
       const float lo_mass = A.want_mass ? ws.m_ref - ZMASS : __builtin_inff();
       lo_f = mk == 0u ? -__builtin_inff() : fminf(fminf(lo_list, lo_cand), lo_mass);
     }
-    int nx = nfull;
+    int nx = sfull;
     if (stream) {
       nx = __builtin_amdgcn_readfirstlane((int)ticket);
-      load_full<DT>(rc.base, V, nx, nx < nfull, lane, X);
+      load_full<DT>(rc.base, V, nx, nx < sfull, lane, X);
     }
     return nx;
   };
@@ -1506,25 +1658,30 @@ __global__ __launch_bounds__(NT) void smp_row(SmpArgs A) {
       s_pos_ok = ok ? 1 : 0;
     }
   }
-  // Chunks [0, nfull) are handed out as the waves free their buffers: wave w
-  // starts with chunks w and w + NW (already requested) and then claims the
-  // next unclaimed chunk, so that a wave slowed by heavy chunks takes fewer
-  // of them. At every step the buffer read is the older of the two in
-  // flight; a claim past nfull ends the wave's stream (claims only grow, so
-  // the other buffer's chunk, claimed earlier, was the smaller).
+  // Chunks [cb, sfull) are handed out as the waves free their buffers: wave
+  // w starts with chunks cb + w and cb + w + NW (already requested) and then
+  // claims the next unclaimed chunk, so that a wave slowed by heavy chunks
+  // takes fewer of them. At every step the buffer read is the older of the
+  // two in flight; a claim past sfull ends the wave's stream (claims only
+  // grow, so the other buffer's chunk, claimed earlier, was the smaller).
+  bool wfirst = true;  // the wave has filtered no chunk yet
   {
-    int c0 = wave, c1 = wave + NW;
-    bool first = true;
-    while (c0 < nfull) {
-      c0 = step(buf0, c0, first, true);
-      first = false;
-      c1 = step(buf1, c1, false, true);  // (c1 may be past the end: then nothing but the claim)
+    int c0 = cb + wave, c1 = cb + wave + NW;
+    while (c0 < sfull) {
+      c0 = step(buf0, c0, wfirst, true, true);
+      wfirst = false;
+      // (c1 may be past the streamed chunks: then nothing but the claim)
+      c1 = step(buf1, c1, false, true, c1 < sfull);
     }
   }
-  // the remaining chunks, each by the wave the round-robin order gives it
-  for (int c = nfull + (wave - nfull % NW + NW) % NW; c < nch; c += NW) {
-    load_chunk<DT, VEC>(rc, V, nch, c, lane, buf0);
-    step(buf0, c, c == wave, false);
+  // the remaining chunks of the segment, round robin over the waves
+  {
+    const int tb = sfull > cb ? sfull : cb;
+    for (int c = tb + wave; c < ce; c += NW) {
+      load_chunk<DT, VEC>(rc, V, nch, c, lane, buf0);
+      step(buf0, c, wfirst, false, true);
+      wfirst = false;
+    }
   }
   // A final bound from the union of the waves' lists: the KB-th largest of
   // their top 8 entries (64 distinct elements). It is at least the minimum
@@ -1576,7 +1733,7 @@ __global__ __launch_bounds__(NT) void smp_row(SmpArgs A) {
       // memory again
       auto fetch = [&](uint32_t (&X)[EPT], uint32_t i) {
         const uint32_t code = fl.def[i].x;
-        if ((code >> 16) == 0u) load_chunk<DT, VEC>(rc, V, nch, (int)(code & 0xffffu), lane, X);
+        if ((code >> 16) == 0u) load_chunk<DT, VEC>(rc, V, nch, (int)(code & 0xffffu), lane, X, false);
       };
       auto redo = [&](uint32_t (&X)[EPT], uint32_t i) {
         const uint32_t code = fl.def[i].x;
@@ -1615,6 +1772,114 @@ __global__ __launch_bounds__(NT) void smp_row(SmpArgs A) {
       }
       __syncthreads();  // the deferred chunks' appends are in LDS
     }
+  }
+
+  // ---- segments: hand the candidates to the row's last block -------------
+  // A segment's certified bound and maximum are no larger than the row's, so
+  // its threshold is no larger than the row's final one: every element of the
+  // row at or above that final threshold is exported by its segment (unless
+  // a segment overflows EXP_CAP: then the row takes the dense path). The
+  // row's top-KB are among the exports, so the last block ranks the union
+  // itself for the final bound.
+  int n_mass = NW;  // mass terms in s_mref / s_mass
+  if (nseg > 1) {
+    const uint32_t mk_s = sh.bw[BW_MKEY];
+    const uint32_t theta_s = A.force_dense ? 0xffffffffu : row_threshold(plan, P, key2f(mk_s), theta);
+    uint64_t* const xc = A.exp_cand + ((int64_t)row * nseg + seg) * EXP_CAP;
+    const uint32_t cnt = sh.count;
+    uint32_t nx;
+    if (cnt <= (uint32_t)BUFCAP) {
+      nx = compact_entries(fl.buf, cnt, xc, EXP_CAP, theta_s, &sh.ctr, true);
+    } else if ((int64_t)(cnt - (uint32_t)BUFCAP) <= spill_share) {
+      compact_entries(fl.buf, BUFCAP, xc, EXP_CAP, theta_s, &sh.ctr, true);
+      nx = compact_entries(spill, cnt - (uint32_t)BUFCAP, xc, EXP_CAP, theta_s, &sh.ctr, false);
+    } else {
+      nx = EXP_CAP + 1u;  // reservations outran the spill share
+    }
+    if (wave == 0) {
+      // the segment's mass relative to its largest wave reference point
+      const float mr = lane < NW ? s_mref[lane] : -__builtin_inff();
+      const uint32_t mkey = wave_max_dpp(mr == -__builtin_inff() ? 0u : f2key(__float_as_uint(mr)));
+      const float mr_s = mkey == 0u ? -__builtin_inff() : key2f(mkey);
+      double t = 0.0;
+      if (lane < NW && mr != -__builtin_inff()) t = s_mass[lane] * exp((double)mr - (double)mr_s);
+      const double ms = wave_sum_f64_dpp(t);
+      if (lane == 0) {
+        SegMeta& m = A.exp_meta[(int64_t)row * nseg + seg];
+        m.count = nx;
+        m.flags = sh.flags;
+        m.mkey = mk_s;
+        m.mass = ms;
+        m.mref = mr_s;
+      }
+    }
+    // release: the barrier completes every wave's stores of the export and
+    // the record; one agent-scope release (an L2 write-back) then publishes
+    // them before the arrival
+    __syncthreads();
+    if (tid == 0) {
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+      const uint32_t old = __hip_atomic_fetch_add(&A.segcnt[row], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      s_last = old == (uint32_t)(nseg - 1) ? 1 : 0;
+      if (s_last) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+    }
+    __syncthreads();
+    if (!s_last) return;  // (uniform: the whole block leaves)
+    // ---- the row's last block: gather every segment's export ---------------
+    const SegMeta* const mt = A.exp_meta + (int64_t)row * nseg;
+    uint32_t* const s_off = (uint32_t*)fl.w;  // per-segment offsets into the buffer, then its counts
+    if (wave == 0) {
+      // lane q reads segment q's record (one round trip for all of them)
+      uint32_t c = 0u, mk = 0u, fo = 0u;
+      float mr = -__builtin_inff();
+      double ms = 0.0;
+      if (lane < nseg) {
+        c = mt[lane].count;
+        mk = mt[lane].mkey;
+        fo = mt[lane].flags;
+        mr = mt[lane].mref;
+        ms = mt[lane].mass;
+        s_mref[lane] = mr;
+        s_mass[lane] = ms;
+      }
+      const bool over = __ballot(lane < nseg && c > (uint32_t)EXP_CAP) != 0ull;
+      const uint32_t cc = c > (uint32_t)EXP_CAP ? 0u : c;
+      const int incl = wave_incl_scan((int)cc, lane);
+      if (lane < nseg) {
+        s_off[lane] = (uint32_t)incl - cc;
+        s_off[SEG_MAX + lane] = cc;
+      }
+      const uint32_t total = (uint32_t)__builtin_amdgcn_readlane(incl, 63);
+      const uint32_t mkr = wave_max_dpp(mk);
+      uint32_t fr = fo;
+#pragma unroll
+      for (int o = 32; o > 0; o >>= 1) fr |= (uint32_t)__shfl_xor((int)fr, o);
+      if (lane == 0) {
+        __hip_atomic_store(&A.segcnt[row], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);  // for the next call
+        sh.bw[BW_MKEY] = mkr;
+        sh.flags = fr;
+        // an overflow sends the row to the dense path (a count past the spill)
+        sh.count = over ? (uint32_t)BUFCAP + (uint32_t)A.dense_ld + 1u : total;
+        sh.ctr = 0u;
+      }
+    }
+    n_mass = nseg;
+    __syncthreads();
+    const uint32_t total = sh.count;
+    if (total <= (uint32_t)BUFCAP) {
+      const uint64_t* const xr = A.exp_cand + (int64_t)row * nseg * EXP_CAP;
+      for (int i = tid; i < nseg * EXP_CAP; i += NT) {
+        const int q = i / EXP_CAP, j = i - q * EXP_CAP;
+        if ((uint32_t)j < s_off[SEG_MAX + q]) fl.buf[s_off[q] + (uint32_t)j] = xr[i];
+      }
+      __syncthreads();
+      theta = total >= (uint32_t)plan.KB
+                  ? lds_kth_key(fl.buf, total, (uint32_t)plan.KB, (uint32_t*)fl.cand, (uint32_t*)fl.cand + 256)
+                  : 0u;
+    } else {
+      theta = 0u;
+    }
+    __syncthreads();
   }
 
   // ---- row results -----------------------------------------------------
@@ -1752,7 +2017,7 @@ __global__ __launch_bounds__(NT) void smp_row(SmpArgs A) {
     double logZ = 0.0;
     if (A.want_mass && wave == 1) {
       double t = 0.0;
-      if (lane < NW && s_mref[lane] != -__builtin_inff()) t = s_mass[lane] * exp((double)s_mref[lane] - (double)M);
+      if (lane < n_mass && s_mref[lane] != -__builtin_inff()) t = s_mass[lane] * exp((double)s_mref[lane] - (double)M);
       logZ = log(wave_sum_f64_dpp(t));
     }
     auto raw_value = [&](uint64_t p) -> float {
@@ -2011,11 +2276,12 @@ __global__ __launch_bounds__(1024) void smp_penalty_prep(PenArgs A) {
 // ---------------------------------------------------------------------------
 template <int DT, bool VEC, bool PEN>
 static hipError_t launch_t(const SmpArgs& a, hipStream_t st) {
-  hipLaunchKernelGGL((smp_row<DT, VEC, PEN>), dim3((unsigned)a.rows), dim3(NT), 0, st, a);
+  hipLaunchKernelGGL((smp_row<DT, VEC, PEN>), dim3((unsigned)(a.rows * a.nseg)), dim3(NT), 0, st, a);
   return hipGetLastError();
 }
 
 hipError_t launch_sample(const SmpArgs& a, int dtype, bool vec, bool pen, hipStream_t st) {
+  if (dtype == 2) return pen ? launch_t<2, false, true>(a, st) : launch_t<2, false, false>(a, st);
   if (dtype == 0) {
     if (vec) return pen ? launch_t<0, true, true>(a, st) : launch_t<0, true, false>(a, st);
     return pen ? launch_t<0, false, true>(a, st) : launch_t<0, false, false>(a, st);

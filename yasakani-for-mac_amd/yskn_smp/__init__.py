@@ -102,6 +102,15 @@ class CAux(C.Structure):
     ]
 
 
+class CHead(C.Structure):
+    _fields_ = [
+        ("acc", C.c_void_p), ("acc_ld", C.c_int64), ("unit_scale", C.c_void_p),
+        ("block_sums", C.c_void_p), ("n_blocks", C.c_int32), ("width", C.c_float),
+        ("epsilon", C.c_float), ("tau", C.c_void_p), ("logits_out", C.c_void_p),
+        ("logits_ld", C.c_int64), ("clear_acc", C.c_int32),
+    ]
+
+
 class CAdvance(C.Structure):
     _fields_ = [("position", C.c_void_p), ("token", C.c_void_p)]
 
@@ -112,6 +121,7 @@ EXPORTED = [
     "yskn_smp_verify", "yskn_smp_sync", "yskn_smp_select_host", "yskn_smp_validate_params",
     "yskn_smp_version", "yskn_smp_get_stats", "yskn_smp_set_params_f64",
     "yskn_smp_validate_params_f64", "yskn_smp_sample_at", "yskn_smp_pm_test",
+    "yskn_smp_sample_head",
 ]
 
 _lib = None
@@ -141,6 +151,7 @@ def load_library(path: str = LIB_PATH) -> C.CDLL:
     L.yskn_smp_sample_at.argtypes = [vp, vp, i32, i32, i32, i64, vp, vp, i32, vp, C.POINTER(CAux),
                                      C.POINTER(CAdvance), vp]
     L.yskn_smp_pm_test.argtypes = [i32, u64, vp, vp, i64]
+    L.yskn_smp_sample_head.argtypes = [vp, C.POINTER(CHead), i32, i32, vp, i32, vp, C.POINTER(CAux), vp]
     L.yskn_smp_sync.argtypes = [vp, vp]
     L.yskn_smp_select_host.argtypes = [vp, vp, i32, u64, C.POINTER(u32)]
     L.yskn_smp_validate_params.argtypes = [C.POINTER(CParams), i32, u32]
@@ -151,7 +162,7 @@ def load_library(path: str = LIB_PATH) -> C.CDLL:
     for name in ("yskn_smp_create", "yskn_smp_set_params", "yskn_smp_sample", "yskn_smp_argmax",
                  "yskn_smp_top_tokens", "yskn_smp_nll", "yskn_smp_verify", "yskn_smp_sync",
                  "yskn_smp_select_host", "yskn_smp_validate_params", "yskn_smp_sample_at",
-                 "yskn_smp_pm_test"):
+                 "yskn_smp_pm_test", "yskn_smp_sample_head"):
         L[name].restype = C.c_int
     _lib = L
     return L
@@ -392,6 +403,34 @@ class DeviceSampler:
                                          base_position.data_ptr(), depth_ptr, row0, out["ids"].data_ptr(),
                                          C.byref(aux), C.byref(adv) if adv is not None else None,
                                          self._stream()))
+        return out
+
+    def sample_head(self, acc, unit_scale, block_sums, tau, positions, *, width=5120.0, epsilon=1e-6,
+                    logits_out=None, clear_acc=False, argmax=False, top8=False, top20=False,
+                    n_logprobs=0, history=None, history_len=None, row_status=False):
+        """yskn_smp_sample_head: sample from the output head's int64
+        accumulators (acc [rows, V] int64, unit_scale [rows] f32, block_sums
+        [rows, n_blocks] f32, tau [V] f32), the logits formed in the sweep."""
+        torch = self.torch
+        if not acc.is_cuda or acc.dim() != 2 or acc.stride(1) != 1 or acc.dtype != torch.int64:
+            raise InvalidInput(EINVAL, "acc must be a 2-D int64 CUDA tensor with unit column stride")
+        rows, V, ld = acc.shape[0], acc.shape[1], acc.stride(0)
+        dev = acc.device
+        pos = positions.to(torch.int64)
+        if pos.dim() == 1:
+            pos = pos.reshape(rows, 1)
+        pos = pos.contiguous()
+        us = unit_scale.to(torch.float32).contiguous()
+        sums = block_sums.to(torch.float32).contiguous()
+        tt = tau.to(torch.float32).contiguous()
+        out = {"ids": torch.empty((rows, pos.shape[1]), dtype=torch.int32, device=dev),
+               "_keep": (pos, us, sums, tt)}
+        aux = self._aux(rows, dev, out, argmax, top8, top20, n_logprobs, history, history_len, row_status)
+        hd = CHead(acc.data_ptr(), ld, us.data_ptr(), sums.data_ptr(), sums.shape[1], width, epsilon,
+                   tt.data_ptr(), _ptr(logits_out), logits_out.stride(0) if logits_out is not None else 0,
+                   1 if clear_acc else 0)
+        _raise(self.L.yskn_smp_sample_head(self.h, C.byref(hd), rows, V, pos.data_ptr(), pos.shape[1],
+                                           out["ids"].data_ptr(), C.byref(aux), self._stream()))
         return out
 
     def argmax(self, logits):
