@@ -285,6 +285,65 @@ int yskn_smp_verify(yskn_smp_handle h, const void* target_logits, int32_t dtype,
                     uint32_t* out_ids, yskn_smp_verify_result* result, const yskn_smp_aux* aux,
                     const yskn_smp_advance* commit, void* stream);
 
+/* ---- Draft-side selection ------------------------------------------------
+ * The drafter's three selection steps, each a pure function of its inputs
+ * (the handle's sampling parameters are not used). rows <= the handle's
+ * max_rows; every row gets a status (yskn_smp_sync reports the first
+ * failure; row_status, when not NULL, receives all of them). */
+
+/* The drafter's shortlist of `count` token ids from its approximate scores:
+ * shortlist() (crates/yskn-ref/src/draft_head.rs:219-282). Two histogram
+ * passes (1,024 bins of the order-preserving key's top 10 bits, then 2,048
+ * bins of the next 11 inside the cut-off bin) fix a 21-bit prefix; every id
+ * above it is kept, in ascending id order, then the lowest ids of the tie
+ * bucket, ascending, up to `count`. Replaces the SHEAD histogram/collect
+ * kernels (src/q35_bdraft.cu:861-898), whose atomic tie-bucket order this
+ * removes (the result is a function of the scores alone).
+ *   scores device [rows x ld] f32; count in 16..=2048, a multiple of 8,
+ *   <= vocab; out_ids device [rows x out_ld] (out_ld >= count).
+ *   Row status YSKN_SMP_ENONFINITE for a non-finite score (its out_ids are
+ *   all 0xffffffff). */
+int yskn_smp_draft_shortlist(yskn_smp_handle h, const float* scores, int32_t rows, int32_t vocab,
+                             int64_t ld, int32_t count, uint32_t* out_ids, int64_t out_ld,
+                             int32_t* row_status, void* stream);
+
+/* The 16 best of n rescored candidates under (score desc, token asc):
+ * top16() (draft_head.rs:284-305); bdr_sk_top16_kernel
+ * (src/q35_bdraft.cu:928). n in 16..=4096. Row status YSKN_SMP_EINVAL
+ * for a non-finite score or a repeated token (outputs 0xffffffff / -inf).
+ *   tokens, scores device [rows x ld]; out_tokens device [rows x 16];
+ *   out_scores device [rows x 16] or NULL (the candidates' own scores). */
+int yskn_smp_draft_top16(yskn_smp_handle h, const uint32_t* tokens, const float* scores,
+                         int32_t rows, int32_t n, int64_t ld, uint32_t* out_tokens,
+                         float* out_scores, int32_t* row_status, void* stream);
+
+/* DraftChoice (draft_head.rs:307-323). */
+typedef struct yskn_smp_draft_choice {
+  int32_t sampled;                  /* 0: DraftChoice::Greedy; 1: Sampled */
+  uint32_t temperature_thousandths; /* Sampled: > 0 (the reference default is 850) */
+  uint64_t seed;                    /* Sampled */
+} yskn_smp_draft_choice;
+
+/* The draft token among 16 candidates per row: choose()
+ * (draft_head.rs:325-379). Greedy: the first strictly larger score in input
+ * order. Sampled: candidates ordered by (score desc, token asc), binary64
+ * temperature 0.001 * thousandths, weights exp_d((s - s_top) / T), members
+ * while the serial prefix before them is below 0.95 * total, then the
+ * largest z + gumbel(seed, positions[row], token) among members, the
+ * earliest winning ties. Replaces the coupling of bdr_select(3)_kernel
+ * (src/q35_bdraft.cu:318-475) with the reference's portable exp_d.
+ *   scores, tokens device [rows x ld] (16 used, ld >= 16)
+ *   positions device [rows] prediction positions (Sampled; may be NULL for
+ *   Greedy); out_tokens device [rows]
+ *   alt, margin, alt3 device [rows] or NULL: the runner-up, the score gap
+ *   to it and the third choice, as launch_bdr_select returns them
+ *   (q35_bdraft.cu:437-450; -1 / 1e30 when absent).
+ *   Row status YSKN_SMP_EINVAL for a non-finite score. */
+int yskn_smp_draft_choose(yskn_smp_handle h, const float* scores, const uint32_t* tokens,
+                          int32_t rows, int64_t ld, const yskn_smp_draft_choice* choice,
+                          const uint64_t* positions, uint32_t* out_tokens, int32_t* alt,
+                          float* margin, int32_t* alt3, int32_t* row_status, void* stream);
+
 /* Synchronise `stream` and return the first per-row error of the handle's
  * last call (YSKN_SMP_OK if none), setting yskn_smp_last_error(). After a
  * verify it returns the pass's status (yskn_smp_verify_result.status). */

@@ -65,6 +65,7 @@ struct yskn_smp {
   int32_t last_rows = 0;
   // the last call was a verify: its pass status is in the caller's result
   const yskn_smp_verify_result* last_verify = nullptr;
+  int last_kind = 0;  // KIND_*: which call's messages yskn_smp_sync reports
 };
 
 namespace {
@@ -277,6 +278,8 @@ bool vector_ok(const void* logits, int32_t dtype, int64_t ld) {
   return ((uintptr_t)logits % 16 == 0) && ((ld * (int64_t)es) % 16 == 0);
 }
 
+enum { KIND_SAMPLE = 0, KIND_SHORTLIST = 1, KIND_TOP16 = 2, KIND_CHOOSE = 3 };
+
 int launch(yskn_smp_handle h, SmpArgs& a, int32_t dtype, bool pen, const yskn_smp_aux* aux,
            hipStream_t st) {
   if (pen) {
@@ -302,6 +305,21 @@ int launch(yskn_smp_handle h, SmpArgs& a, int32_t dtype, bool pen, const yskn_sm
   if (e != hipSuccess) return hip_fail(e, "sampler launch");
   h->last_rows = a.rows;
   h->last_verify = a.mode == MODE_VERIFY ? (const yskn_smp_verify_result*)a.vresult : nullptr;
+  h->last_kind = KIND_SAMPLE;
+  return YSKN_SMP_OK;
+}
+
+int draft_rows(yskn_smp_handle h, int32_t rows) {
+  if (!h) return fail(YSKN_SMP_EINVAL, "invalid input: null handle");
+  if (rows <= 0 || rows > h->max_rows) return fail(YSKN_SMP_ERANGE, "rows outside 1..=max_rows");
+  return YSKN_SMP_OK;
+}
+
+int draft_launched(yskn_smp_handle h, hipError_t e, int32_t rows, int kind) {
+  if (e != hipSuccess) return hip_fail(e, "draft selection launch");
+  h->last_rows = rows;
+  h->last_verify = nullptr;
+  h->last_kind = kind;
   return YSKN_SMP_OK;
 }
 
@@ -634,6 +652,87 @@ int yskn_smp_verify(yskn_smp_handle h, const void* target_logits, int32_t dtype,
   return launch(h, a, dtype, pen, aux, (hipStream_t)stream);
 }
 
+int yskn_smp_draft_shortlist(yskn_smp_handle h, const float* scores, int32_t rows, int32_t vocab,
+                             int64_t ld, int32_t count, uint32_t* out_ids, int64_t out_ld,
+                             int32_t* row_status, void* stream) {
+  int st = draft_rows(h, rows);
+  if (st) return st;
+  if (!scores || !out_ids) return fail(YSKN_SMP_EINVAL, "invalid input: null scores or output");
+  if (vocab <= 0) return fail(YSKN_SMP_EINVAL, "invalid input: empty vocabulary");
+  if (ld < vocab) return fail(YSKN_SMP_EINVAL, "invalid input: ld < vocab");
+  if (count < 16 || count > 2048 || count % 8 != 0 || count > vocab)
+    return fail(YSKN_SMP_EINVAL, "invalid input: shortlist must be 16..2048, multiple of 8 and <= vocabulary");
+  if (out_ld < count) return fail(YSKN_SMP_EINVAL, "invalid input: out_ld < count");
+  DraftShortlistArgs a;
+  std::memset(&a, 0, sizeof a);
+  a.scores = scores;
+  a.ld = ld;
+  a.V = vocab;
+  a.rows = rows;
+  a.count = count;
+  a.out = out_ids;
+  a.out_ld = out_ld;
+  a.status = h->d_status;
+  a.row_status = row_status;
+  return draft_launched(h, launch_draft_shortlist(a, (hipStream_t)stream), rows, KIND_SHORTLIST);
+}
+
+int yskn_smp_draft_top16(yskn_smp_handle h, const uint32_t* tokens, const float* scores,
+                         int32_t rows, int32_t n, int64_t ld, uint32_t* out_tokens,
+                         float* out_scores, int32_t* row_status, void* stream) {
+  int st = draft_rows(h, rows);
+  if (st) return st;
+  if (!tokens || !scores || !out_tokens) return fail(YSKN_SMP_EINVAL, "invalid input: null candidates or output");
+  if (n < 16) return fail(YSKN_SMP_EINVAL, "invalid input: top16 requires >=16 finite candidates");
+  if (n > TOP16_NMAX) return fail(YSKN_SMP_ERANGE, "top16 takes at most 4,096 candidates per row");
+  if (ld < n) return fail(YSKN_SMP_EINVAL, "invalid input: ld < n");
+  DraftTop16Args a;
+  std::memset(&a, 0, sizeof a);
+  a.tokens = tokens;
+  a.scores = scores;
+  a.ld = ld;
+  a.n = n;
+  a.rows = rows;
+  a.out_tokens = out_tokens;
+  a.out_scores = out_scores;
+  a.status = h->d_status;
+  a.row_status = row_status;
+  return draft_launched(h, launch_draft_top16(a, (hipStream_t)stream), rows, KIND_TOP16);
+}
+
+int yskn_smp_draft_choose(yskn_smp_handle h, const float* scores, const uint32_t* tokens,
+                          int32_t rows, int64_t ld, const yskn_smp_draft_choice* choice,
+                          const uint64_t* positions, uint32_t* out_tokens, int32_t* alt,
+                          float* margin, int32_t* alt3, int32_t* row_status, void* stream) {
+  int st = draft_rows(h, rows);
+  if (st) return st;
+  if (!scores || !tokens || !out_tokens || !choice)
+    return fail(YSKN_SMP_EINVAL, "invalid input: null candidates, choice or output");
+  if (ld < 16) return fail(YSKN_SMP_EINVAL, "invalid input: choice needs 16 finite candidates");
+  const bool sampled = choice->sampled != 0;
+  if (sampled && choice->temperature_thousandths == 0)
+    return fail(YSKN_SMP_EINVAL, "invalid input: draft temperature must be positive");
+  if (sampled && !positions) return fail(YSKN_SMP_EINVAL, "invalid input: a sampled choice needs positions");
+  DraftChooseArgs a;
+  std::memset(&a, 0, sizeof a);
+  a.scores = scores;
+  a.tokens = tokens;
+  a.ld = ld;
+  a.rows = rows;
+  a.sampled = sampled ? 1 : 0;
+  a.seed = choice->seed;
+  // a binary64 multiply, not a division (draft_head.rs:354-356)
+  a.temperature = 0.001 * (double)choice->temperature_thousandths;
+  a.positions = positions;
+  a.out = out_tokens;
+  a.alt = alt;
+  a.margin = margin;
+  a.alt3 = alt3;
+  a.status = h->d_status;
+  a.row_status = row_status;
+  return draft_launched(h, launch_draft_choose(a, (hipStream_t)stream), rows, KIND_CHOOSE);
+}
+
 int yskn_smp_sync(yskn_smp_handle h, void* stream) {
   if (!h) return fail(YSKN_SMP_EINVAL, "invalid input: null handle");
   hipError_t e = hipStreamSynchronize((hipStream_t)stream);
@@ -651,6 +750,12 @@ int yskn_smp_sync(yskn_smp_handle h, void* stream) {
     s.assign(1, r.status);
   }
   for (int32_t v : s) {
+    if (v == YSKN_SMP_OK) continue;
+    // the reference's messages (draft_head.rs:240-249,285-300,326-336)
+    if (h->last_kind == KIND_SHORTLIST) return fail(v, "non-finite value in draft approximate scores");
+    if (h->last_kind == KIND_TOP16)
+      return fail(v, "invalid input: top16 requires >=16 finite candidates and no duplicate draft candidates");
+    if (h->last_kind == KIND_CHOOSE) return fail(v, "invalid input: choice needs 16 finite candidates");
     if (v == YSKN_SMP_ENONFINITE) return fail(v, "non-finite value in logits");
     if (v == YSKN_SMP_EINVAL)
       return fail(v, "invalid input: token outside the vocabulary, invalid history or prediction position overflow");

@@ -178,8 +178,55 @@ struct PenArgs {
   int32_t prm_shared;
 };
 
-// Host-side launchers (smp_kernels.hip).
+// Draft-side selection (smp_draft.hip).
+constexpr int TOP16_NMAX = 4096;  // candidates per row of the top-16 kernel
+
+struct DraftShortlistArgs {
+  const float* scores;  // [rows][ld]
+  int64_t ld;
+  int32_t V;
+  int32_t rows;
+  int32_t count;
+  uint32_t* out;  // [rows][out_ld]
+  int64_t out_ld;
+  int32_t* status;      // [rows], always written
+  int32_t* row_status;  // [rows] or NULL
+};
+
+struct DraftTop16Args {
+  const uint32_t* tokens;  // [rows][ld]
+  const float* scores;     // [rows][ld]
+  int64_t ld;
+  int32_t n;
+  int32_t rows;
+  uint32_t* out_tokens;  // [rows][16]
+  float* out_scores;     // [rows][16] or NULL
+  int32_t* status;
+  int32_t* row_status;
+};
+
+struct DraftChooseArgs {
+  const float* scores;     // [rows][ld], 16 used
+  const uint32_t* tokens;  // [rows][ld], 16 used
+  int64_t ld;
+  int32_t rows;
+  int32_t sampled;
+  uint64_t seed;
+  double temperature;        // 0.001 * thousandths, binary64
+  const uint64_t* positions;  // [rows] (sampled only)
+  uint32_t* out;             // [rows]
+  int32_t* alt;              // [rows] or NULL
+  float* margin;             // [rows] or NULL
+  int32_t* alt3;             // [rows] or NULL
+  int32_t* status;
+  int32_t* row_status;
+};
+
+// Host-side launchers (smp_kernels.hip, smp_draft.hip).
 hipError_t launch_sample(const SmpArgs& a, int dtype, bool vec, bool pen, hipStream_t st);
 hipError_t launch_penalty_prep(const PenArgs& a, hipStream_t st);
+hipError_t launch_draft_shortlist(const DraftShortlistArgs& a, hipStream_t st);
+hipError_t launch_draft_top16(const DraftTop16Args& a, hipStream_t st);
+hipError_t launch_draft_choose(const DraftChooseArgs& a, hipStream_t st);
 
 }  // namespace yskn

@@ -102,6 +102,10 @@ class CAux(C.Structure):
     ]
 
 
+class CDraftChoice(C.Structure):
+    _fields_ = [("sampled", C.c_int32), ("temperature_thousandths", C.c_uint32), ("seed", C.c_uint64)]
+
+
 class CHead(C.Structure):
     _fields_ = [
         ("acc", C.c_void_p), ("acc_ld", C.c_int64), ("unit_scale", C.c_void_p),
@@ -121,7 +125,7 @@ EXPORTED = [
     "yskn_smp_verify", "yskn_smp_sync", "yskn_smp_select_host", "yskn_smp_validate_params",
     "yskn_smp_version", "yskn_smp_get_stats", "yskn_smp_set_params_f64",
     "yskn_smp_validate_params_f64", "yskn_smp_sample_at", "yskn_smp_pm_test",
-    "yskn_smp_sample_head",
+    "yskn_smp_sample_head", "yskn_smp_draft_shortlist", "yskn_smp_draft_top16", "yskn_smp_draft_choose",
 ]
 
 _lib = None
@@ -152,6 +156,10 @@ def load_library(path: str = LIB_PATH) -> C.CDLL:
                                      C.POINTER(CAdvance), vp]
     L.yskn_smp_pm_test.argtypes = [i32, u64, vp, vp, i64]
     L.yskn_smp_sample_head.argtypes = [vp, C.POINTER(CHead), i32, i32, vp, i32, vp, C.POINTER(CAux), vp]
+    L.yskn_smp_draft_shortlist.argtypes = [vp, vp, i32, i32, i64, i32, vp, i64, vp, vp]
+    L.yskn_smp_draft_top16.argtypes = [vp, vp, vp, i32, i32, i64, vp, vp, vp, vp]
+    L.yskn_smp_draft_choose.argtypes = [vp, vp, vp, i32, i64, C.POINTER(CDraftChoice), vp, vp, vp, vp, vp,
+                                        vp, vp]
     L.yskn_smp_sync.argtypes = [vp, vp]
     L.yskn_smp_select_host.argtypes = [vp, vp, i32, u64, C.POINTER(u32)]
     L.yskn_smp_validate_params.argtypes = [C.POINTER(CParams), i32, u32]
@@ -162,7 +170,8 @@ def load_library(path: str = LIB_PATH) -> C.CDLL:
     for name in ("yskn_smp_create", "yskn_smp_set_params", "yskn_smp_sample", "yskn_smp_argmax",
                  "yskn_smp_top_tokens", "yskn_smp_nll", "yskn_smp_verify", "yskn_smp_sync",
                  "yskn_smp_select_host", "yskn_smp_validate_params", "yskn_smp_sample_at",
-                 "yskn_smp_pm_test", "yskn_smp_sample_head"):
+                 "yskn_smp_pm_test", "yskn_smp_sample_head", "yskn_smp_draft_shortlist",
+                 "yskn_smp_draft_top16", "yskn_smp_draft_choose"):
         L[name].restype = C.c_int
     _lib = L
     return L
@@ -485,6 +494,67 @@ class DeviceSampler:
                                       ids.data_ptr(), res.data_ptr(), C.byref(aux),
                                       C.byref(adv) if adv is not None else None, self._stream()))
         return ids, res, (d, bp, eos, outs)
+
+    # ---- draft-side selection (draft_head.rs:219-379) ----
+    def _rows2d(self, t, dtype, what):
+        torch = self.torch
+        if not t.is_cuda or t.dim() != 2 or t.stride(1) != 1 or t.dtype != dtype:
+            raise InvalidInput(EINVAL, f"{what} must be a 2-D {dtype} CUDA tensor with unit column stride")
+        return t.shape[0], t.shape[1], t.stride(0)
+
+    def draft_shortlist(self, scores, count: int, row_status=False):
+        """shortlist() per row of scores [rows, V] f32: count ids [rows, count]."""
+        torch = self.torch
+        rows, V, ld = self._rows2d(scores, torch.float32, "scores")
+        out = {"ids": torch.empty((rows, max(count, 1)), dtype=torch.int32, device=scores.device)}
+        if row_status:
+            out["status"] = torch.empty(rows, dtype=torch.int32, device=scores.device)
+        _raise(self.L.yskn_smp_draft_shortlist(self.h, scores.data_ptr(), rows, V, ld, count,
+                                               out["ids"].data_ptr(), out["ids"].stride(0),
+                                               _ptr(out.get("status")), self._stream()))
+        return out
+
+    def draft_top16(self, tokens, scores, row_status=False):
+        """top16() per row of (tokens [rows, n] int32, scores [rows, n] f32)."""
+        torch = self.torch
+        rows, n, ld = self._rows2d(scores, torch.float32, "scores")
+        if tuple(tokens.shape) != (rows, n) or tokens.stride() != scores.stride() or tokens.dtype != torch.int32:
+            raise InvalidInput(EINVAL, "tokens must be int32 and laid out like scores")
+        out = {"tokens": torch.empty((rows, 16), dtype=torch.int32, device=scores.device),
+               "scores": torch.empty((rows, 16), dtype=torch.float32, device=scores.device)}
+        if row_status:
+            out["status"] = torch.empty(rows, dtype=torch.int32, device=scores.device)
+        _raise(self.L.yskn_smp_draft_top16(self.h, tokens.data_ptr(), scores.data_ptr(), rows, n, ld,
+                                           out["tokens"].data_ptr(), out["scores"].data_ptr(),
+                                           _ptr(out.get("status")), self._stream()))
+        return out
+
+    def draft_choose(self, scores, tokens, *, sampled=True, seed=0, temperature_thousandths=850,
+                     positions=None, alternates=False, row_status=False):
+        """choose() per row of 16 candidates (scores [rows, >=16] f32, tokens
+        int32 alike); positions int64 [rows] for a sampled choice."""
+        torch = self.torch
+        rows, n, ld = self._rows2d(scores, torch.float32, "scores")
+        if tuple(tokens.shape) != (rows, n) or tokens.stride() != scores.stride() or tokens.dtype != torch.int32:
+            raise InvalidInput(EINVAL, "tokens must be int32 and laid out like scores")
+        dev = scores.device
+        out = {"token": torch.empty(rows, dtype=torch.int32, device=dev)}
+        if alternates:
+            out["alt"] = torch.empty(rows, dtype=torch.int32, device=dev)
+            out["margin"] = torch.empty(rows, dtype=torch.float32, device=dev)
+            out["alt3"] = torch.empty(rows, dtype=torch.int32, device=dev)
+        if row_status:
+            out["status"] = torch.empty(rows, dtype=torch.int32, device=dev)
+        pos = None
+        if positions is not None:
+            pos = positions.to(device=dev, dtype=torch.int64).contiguous()
+            out["_pos"] = pos
+        ch = CDraftChoice(1 if sampled else 0, temperature_thousandths, seed & 0xFFFFFFFFFFFFFFFF)
+        _raise(self.L.yskn_smp_draft_choose(self.h, scores.data_ptr(), tokens.data_ptr(), rows, ld, C.byref(ch),
+                                            _ptr(pos), out["token"].data_ptr(), _ptr(out.get("alt")),
+                                            _ptr(out.get("margin")), _ptr(out.get("alt3")),
+                                            _ptr(out.get("status")), self._stream()))
+        return out
 
     def sync(self) -> None:
         _raise(self.L.yskn_smp_sync(self.h, self._stream()))
