@@ -1202,13 +1202,6 @@ __device__ __forceinline__ void chunk_values(const RowCtx& rc, int32_t V, int c,
   }
 }
 
-// Appended candidates go to per-wave blocks of ABLK slots of the append
-// buffer (slots past BUFCAP are in the row's spill area): a wave reserves a
-// block with one LDS atomic and fills it in order, so the common append
-// costs no atomic. Slots a wave leaves unused are cleared to 0 (key 0 is
-// below every threshold).
-constexpr uint32_t ABLK = 64;
-
 // The first NSTASH deferred chunks keep their converted values in LDS, in
 // the candidate and weight arrays (unused until the finish): their second
 // pass reads LDS instead of memory. Slot s holds lane l's values
@@ -1244,31 +1237,8 @@ struct WaveState {
   float m_ref;      // reference point of the wave's logprob mass (uniform)
   double acc;       // per lane: sum of exp(l - m_ref) over l >= m_ref - ZMASS
   bool bad;         // per lane: a non-finite value was seen
-  uint32_t ab_cur;  // next free slot of the wave's append block (uniform)
-  uint32_t ab_end;  // end of that block
   uint32_t spill_cap;  // slots of the row's spill area
 };
-
-// Entry e (per lane, where k) to slot `slot` of the append buffer or, past
-// BUFCAP, of the spill area (reservations past the spill area are dropped:
-// the finish then takes the dense path).
-__device__ __forceinline__ void put_entry(RowLds& fl, uint64_t* spill, uint32_t spill_cap, uint32_t slot,
-                                          uint64_t e, bool k, bool& spilled) {
-  if (k && slot < (uint32_t)BUFCAP) ((lds_u64*)fl.buf)[slot] = e;
-  if (k && slot >= (uint32_t)BUFCAP && slot - (uint32_t)BUFCAP < spill_cap) {
-    __builtin_nontemporal_store(e, &((global_u64*)spill)[slot - BUFCAP]);
-    spilled = true;
-  }
-}
-
-// Clears the rest of the wave's append block.
-__device__ __forceinline__ void close_block(WaveState& ws, RowLds& fl, uint64_t* spill, int lane, bool& spilled) {
-  for (uint32_t s0 = ws.ab_cur; s0 < ws.ab_end; s0 += 64) {
-    const uint32_t slot = s0 + (uint32_t)lane;
-    put_entry(fl, spill, ws.spill_cap, slot, 0ull, slot < ws.ab_end, spilled);
-  }
-  ws.ab_cur = ws.ab_end;
-}
 
 // Shared streaming state of a row block.
 // The bounds the waves share sit in one array so that a wave reads all of
@@ -1288,11 +1258,50 @@ struct RowShared {
   uint32_t next;       // next chunk of the stream not yet claimed by a wave
 };
 
+// The element pass of chunk_filter: mass terms of the values >= lo, and
+// the values >= thf (when keep) appended in order from slot slot0. With
+// SPILL the slots reach past BUFCAP: those go to the row's spill area
+// (dropped past its end, which sends the row to the dense path). The
+// common chunk takes the LDS-only copy, which holds no global store.
+template <int GRP, int NGRP, bool SPILL>
+__device__ __forceinline__ void chunk_pass(const uint32_t (&kb)[EPT], const float (&gmax)[NGRP], float tany,
+                                           float lo, float thf, bool keep, uint32_t eb, uint32_t slot0,
+                                           WaveState& ws, RowLds& fl, uint64_t* spill) {
+  uint32_t cur = slot0;
+#pragma unroll
+  for (int q = 0; q < NGRP; ++q) {
+    if (!__ballot(gmax[q] >= tany)) continue;
+#pragma unroll
+    for (int j = 0; j < GRP; ++j) {
+      const float v = __uint_as_float(kb[q * GRP + j]);
+      if (!__ballot(v >= tany)) continue;
+      if (v >= lo) ws.acc += (double)__builtin_amdgcn_exp2f((v - ws.m_ref) * 1.4426950408889634f);
+      if (keep) {
+        const bool k = v >= thf;
+        const uint64_t km = __ballot(k);
+        if (km) {
+          const uint32_t slot = cur + lanes_below(km);
+          if (k) {
+            const uint64_t e = pack(f2key(__float_as_uint(v)), eb + (uint32_t)(q * 64 * GRP + j));
+            if (!SPILL || slot < (uint32_t)BUFCAP) {
+              ((lds_u64*)fl.buf)[slot] = e;
+            } else if (slot - (uint32_t)BUFCAP < ws.spill_cap) {
+              __builtin_nontemporal_store(e, &((global_u64*)spill)[slot - BUFCAP]);
+            }
+          }
+          cur += (uint32_t)__popcll(km);
+        }
+      }
+    }
+  }
+}
+
 // Mass terms (if mass) and candidates of chunk c for threshold thr. Work is
 // skipped per chunk (its maximum), then per load group (GRP consecutive
 // values of a lane), then per element slot, wherever no lane holds a value
 // >= min(threshold, m_ref - ZMASS); the chunk's survivors are counted first
-// and reserve their slots with one LDS atomic. Mass terms are binary32
+// and reserve their slots with one LDS atomic (the buffer has no holes).
+// Mass terms are binary32
 // exponentials accumulated in binary64: next to the row maximum's term (1.0)
 // the small terms must not be rounded away, since the top token's logprob is
 // -log(1 + their sum). Slots beyond BUFCAP go to the row's spill area in
@@ -1355,39 +1364,27 @@ __device__ __forceinline__ void chunk_filter(int c, int lane, const uint32_t (&k
     }
   }
   const uint32_t eb = (uint32_t)c * WSEG + (uint32_t)lane * GRP;
-  bool spilled = false;
+  uint32_t base = 0u, total = 0u;
+  if (keep_any) {
 #pragma unroll
-  for (int q = 0; q < NGRP; ++q) {
-    if (!__ballot(gmax[q] >= tany)) continue;
+    for (int q = 0; q < NGRP; ++q) {
+      if (!__ballot(gmax[q] >= thf)) continue;
 #pragma unroll
-    for (int j = 0; j < GRP; ++j) {
-      const float v = __uint_as_float(kb[q * GRP + j]);
-      if (!__ballot(v >= tany)) continue;
-      if (v >= lo) ws.acc += (double)__builtin_amdgcn_exp2f((v - ws.m_ref) * 1.4426950408889634f);
-      if (keep_any) {
-        const bool k = v >= thf;
-        const uint64_t km = __ballot(k);
-        if (km) {
-          const uint32_t n = (uint32_t)__popcll(km);
-          if (ws.ab_cur + n > ws.ab_end) {
-            // the block is full: clear its rest, reserve the next
-            close_block(ws, fl, spill, lane, spilled);
-            uint32_t base = 0u;
-            if (lane == 0) base = atomicAdd(&sh.count, ABLK);
-            base = (uint32_t)__builtin_amdgcn_readfirstlane((int)base);
-            ws.ab_cur = base;
-            ws.ab_end = base + ABLK;
-          }
-          const uint64_t e = pack(f2key(__float_as_uint(v)), eb + (uint32_t)(q * 64 * GRP + j));
-          put_entry(fl, spill, ws.spill_cap, ws.ab_cur + lanes_below(km), e, k, spilled);
-          ws.ab_cur += n;
-        }
-      }
+      for (int j = 0; j < GRP; ++j) total += (uint32_t)__popcll(__ballot(__uint_as_float(kb[q * GRP + j]) >= thf));
+    }
+    if (total) {
+      if (lane == 0) base = atomicAdd(&sh.count, total);
+      base = (uint32_t)__builtin_amdgcn_readfirstlane((int)base);
     }
   }
-  // the rare spill stores end with a full wait, so the common path holds
-  // only LDS stores and the compiler keeps the prefetched chunk in flight
-  if (spilled) __builtin_amdgcn_s_waitcnt(0);
+  if (base + total <= (uint32_t)BUFCAP) {
+    chunk_pass<GRP, NGRP, false>(kb, gmax, tany, lo, thf, keep_any, eb, base, ws, fl, spill);
+  } else {
+    chunk_pass<GRP, NGRP, true>(kb, gmax, tany, lo, thf, keep_any, eb, base, ws, fl, spill);
+    // the rare spill stores end with a full wait, so the common path holds
+    // only LDS stores and the compiler keeps the prefetched chunk in flight
+    __builtin_amdgcn_s_waitcnt(0);
+  }
 }
 
 // Order-free parallel compaction: appends to dst the entries of src[0, n)
@@ -1506,8 +1503,6 @@ __global__ __launch_bounds__(NT) void smp_row(SmpArgs A) {
   ws.m_ref = -__builtin_inff();
   ws.acc = 0.0;
   ws.bad = false;
-  ws.ab_cur = 0u;
-  ws.ab_end = 0u;
   ws.spill_cap = (uint32_t)spill_share;
   __syncthreads();  // shared state initialised
 
@@ -1690,11 +1685,6 @@ __global__ __launch_bounds__(NT) void smp_row(SmpArgs A) {
   // final one (every improvement was published), which keeps the buffer
   // complete down to it.
   if (lane < 8) fl.lists[wave * 8 + lane] = lane < plan.KB ? lst : 0u;
-  {
-    bool sp = false;
-    close_block(ws, fl, spill, lane, sp);
-    if (sp) __builtin_amdgcn_s_waitcnt(0);
-  }
   // The wave's own results, which the deferred reads below do not change
   // (they add no mass terms and find no new maximum).
   if (__ballot(ws.bad)) wflags |= F_NONFINITE;
@@ -1764,11 +1754,6 @@ __global__ __launch_bounds__(NT) void smp_row(SmpArgs A) {
         if (id < nd) fetch(buf1, id);
         ia = ic;
         ib = id;
-      }
-      {
-        bool sp = false;
-        close_block(ws, fl, spill, lane, sp);
-        if (sp) __builtin_amdgcn_s_waitcnt(0);
       }
       __syncthreads();  // the deferred chunks' appends are in LDS
     }
