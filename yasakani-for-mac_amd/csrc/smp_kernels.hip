@@ -1268,30 +1268,45 @@ __device__ __forceinline__ void chunk_pass(const uint32_t (&kb)[EPT], const floa
                                            float lo, float thf, bool keep, uint32_t eb, uint32_t slot0,
                                            WaveState& ws, RowLds& fl, uint64_t* spill) {
   uint32_t cur = slot0;
+  const bool mass = lo != __builtin_inff();
 #pragma unroll
   for (int q = 0; q < NGRP; ++q) {
     if (!__ballot(gmax[q] >= tany)) continue;
+    if (mass) {
+      // the group's mass terms, independent of one another (no branch, no
+      // serial chain through the accumulator): a binary64 pairwise sum,
+      // then one add to the lane's accumulator
+      double t[GRP];
+#pragma unroll
+      for (int j = 0; j < GRP; ++j) {
+        const float v = __uint_as_float(kb[q * GRP + j]);
+        const float e = __builtin_amdgcn_exp2f((v - ws.m_ref) * 1.4426950408889634f);
+        t[j] = v >= lo ? (double)e : 0.0;
+      }
+#pragma unroll
+      for (int h = GRP / 2; h > 0; h >>= 1) {
+#pragma unroll
+        for (int j = 0; j < h; ++j) t[j] = t[j] + t[j + h];
+      }
+      ws.acc += t[0];
+    }
+    if (!keep) continue;
 #pragma unroll
     for (int j = 0; j < GRP; ++j) {
       const float v = __uint_as_float(kb[q * GRP + j]);
-      if (!__ballot(v >= tany)) continue;
-      if (v >= lo) ws.acc += (double)__builtin_amdgcn_exp2f((v - ws.m_ref) * 1.4426950408889634f);
-      if (keep) {
-        const bool k = v >= thf;
-        const uint64_t km = __ballot(k);
-        if (km) {
-          const uint32_t slot = cur + lanes_below(km);
-          if (k) {
-            const uint64_t e = pack(f2key(__float_as_uint(v)), eb + (uint32_t)(q * 64 * GRP + j));
-            if (!SPILL || slot < (uint32_t)BUFCAP) {
-              ((lds_u64*)fl.buf)[slot] = e;
-            } else if (slot - (uint32_t)BUFCAP < ws.spill_cap) {
-              __builtin_nontemporal_store(e, &((global_u64*)spill)[slot - BUFCAP]);
-            }
-          }
-          cur += (uint32_t)__popcll(km);
+      const bool k = v >= thf;
+      const uint64_t km = __ballot(k);
+      if (!km) continue;
+      const uint32_t slot = cur + lanes_below(km);
+      if (k) {
+        const uint64_t e = pack(f2key(__float_as_uint(v)), eb + (uint32_t)(q * 64 * GRP + j));
+        if (!SPILL || slot < (uint32_t)BUFCAP) {
+          ((lds_u64*)fl.buf)[slot] = e;
+        } else if (slot - (uint32_t)BUFCAP < ws.spill_cap) {
+          __builtin_nontemporal_store(e, &((global_u64*)spill)[slot - BUFCAP]);
         }
       }
+      cur += (uint32_t)__popcll(km);
     }
   }
 }
