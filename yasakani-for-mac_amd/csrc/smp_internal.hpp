@@ -16,7 +16,7 @@ constexpr int WSEG = 64 * EPT;     // elements per chunk
 constexpr int CAP = 4096;          // candidates a row block sorts in LDS
 constexpr int BUFCAP = 8192;       // candidates a row block's append buffer holds
 constexpr int DLANES = 16;         // lanes with survivors above which a chunk is deferred
-constexpr int DEFCAP = 1024;       // deferred chunks a row block records
+constexpr int DEFCAP = 512;        // deferred chunks a row block records
 constexpr int KBMAX = 64;          // largest "small" top-k / list length
 // Segments: a row split over several blocks exports, per segment, every
 // candidate at or above the segment's own certified threshold (at most

@@ -1038,7 +1038,7 @@ struct RowLds {
   uint64_t buf[BUFCAP];    // append buffer of candidates (unordered)
   uint64_t cand[CAP];      // the candidates that pass the final bounds, sorted
   double w[CAP];           // weights of the tail; scratch of the sorts
-  uint2 def[DEFCAP];           // deferred chunks: (chunk, its largest key)
+  uint4 def[DEFCAP];           // deferred chunks: (chunk, largest key, second key, id of the largest)
   uint32_t lists[NW * 8];      // each wave's 8 largest list entries, after the stream
 };
 
@@ -1366,13 +1366,33 @@ __device__ __forceinline__ void chunk_filter(int c, int lane, const uint32_t (&k
     idx = (uint32_t)__builtin_amdgcn_readfirstlane((int)idx);
     if (idx < (uint32_t)DEFCAP) {
       if (cmax == 0u) cmax = wave_max_dpp(lk);
+      // The chunk's two largest keys and the id of the largest: after the
+      // stream it is read again only if the second reaches the final bound
+      // (when only the largest does, that one element is appended then).
+      // Per lane: its largest value, where it is, and its second (a value
+      // equal to the largest counts as the second).
+      float m1 = -__builtin_inff(), m2 = -__builtin_inff();
+      int p1 = 0;
+#pragma unroll
+      for (int e = 0; e < EPT; ++e) {
+        const float v = __uint_as_float(kb[e]);
+        const bool up = v > m1;
+        m2 = up ? m1 : fmaxf(m2, v);
+        p1 = up ? e : p1;
+        m1 = up ? v : m1;
+      }
+      const int L = (int)__builtin_ctzll(__ballot(lk == cmax));  // a lane holding the chunk maximum
+      const uint32_t k2 = m2 == -__builtin_inff() ? 0u : f2key(__float_as_uint(m2));
+      const uint32_t sec = wave_max_dpp(lane == L ? k2 : lk);
+      const uint32_t pos = (uint32_t)(c * WSEG + lane * GRP + (p1 / GRP) * 64 * GRP + p1 % GRP);
+      const uint32_t id1 = (uint32_t)__builtin_amdgcn_readlane((int)pos, L);
       // (chunk, stash slot + 1 or 0) in the record's first word
       uint32_t code = (uint32_t)c;
       if (idx < NSTASH) {
         stash_chunk(fl, idx, lane, kb);
         code |= (idx + 1u) << 16;
       }
-      if (lane == 0) fl.def[idx] = make_uint2(code, cmax);
+      if (lane == 0) fl.def[idx] = make_uint4(code, cmax, sec, id1);
       keep_any = false;
       tany = lo;
       if (!(key2f(cmax) >= tany)) return;
@@ -1700,7 +1720,7 @@ __global__ __launch_bounds__(NT) void smp_row(SmpArgs A) {
   // final one (every improvement was published), which keeps the buffer
   // complete down to it.
   if (lane < 8) fl.lists[wave * 8 + lane] = lane < plan.KB ? lst : 0u;
-  // The wave's own results, which the deferred reads below do not change
+  // The wave's own results, which the deferred chunks below do not change
   // (they add no mass terms and find no new maximum).
   if (__ballot(ws.bad)) wflags |= F_NONFINITE;
   {
@@ -1718,20 +1738,47 @@ __global__ __launch_bounds__(NT) void smp_row(SmpArgs A) {
     const uint32_t t = wave_kth_largest_radix(fl.lists[lane], plan.KB);
     theta = t > theta ? t : theta;
   }
-  // deferred chunks whose largest key reaches the final bound: read again
-  // and filter with that bound. Entry i belongs to wave i % NW; each wave
-  // keeps two of its chunks in flight (the stream's buffers are free now).
+  // Deferred chunks against the final bound: one whose second largest key
+  // reaches it is read again and filtered with that bound; one where only
+  // its largest does hands that element over directly (wave 0); the rest
+  // hold nothing at or above it. Entry i is read again by wave i % NW; each
+  // wave keeps two of its chunks in flight (the stream's buffers are free).
   if (!A.force_dense) {
     const uint32_t mkf = sh.bw[BW_MKEY];
     const uint32_t thr_f = row_threshold(plan, P, key2f(mkf), theta);
     const uint32_t nd = sh.ndef < (uint32_t)DEFCAP ? sh.ndef : (uint32_t)DEFCAP;
+    if (wave == 0) {
+      bool spilled = false;
+      for (uint32_t i0 = 0; i0 < nd; i0 += 64) {
+        const uint32_t i = i0 + (uint32_t)lane;
+        const uint4 d = i < nd ? fl.def[i] : make_uint4(0u, 0u, 0u, 0u);
+        const bool one = i < nd && d.y >= thr_f && d.z < thr_f;
+        const uint64_t m = __ballot(one);
+        if (m) {
+          uint32_t base = 0u;
+          if (lane == 0) base = atomicAdd(&sh.count, (uint32_t)__popcll(m));
+          base = (uint32_t)__builtin_amdgcn_readfirstlane((int)base);
+          const uint32_t slot = base + lanes_below(m);
+          if (one) {
+            const uint64_t e = pack(d.y, d.w);
+            if (slot < (uint32_t)BUFCAP) {
+              ((lds_u64*)fl.buf)[slot] = e;
+            } else if (slot - (uint32_t)BUFCAP < ws.spill_cap) {
+              __builtin_nontemporal_store(e, &((global_u64*)spill)[slot - BUFCAP]);
+              spilled = true;
+            }
+          }
+        }
+      }
+      if (__ballot(spilled)) __builtin_amdgcn_s_waitcnt(0);
+    }
     // (every wave sees the same entries: the condition is block-uniform)
     bool any = false;
-    for (uint32_t i = (uint32_t)lane; i < nd; i += 64) any = any || fl.def[i].y >= thr_f;
+    for (uint32_t i = (uint32_t)lane; i < nd; i += 64) any = any || fl.def[i].z >= thr_f;
     if (__ballot(any)) {
       auto next = [&](uint32_t from) -> uint32_t {
         for (uint32_t i = from; i < nd; i += NW)
-          if (fl.def[i].y >= thr_f) return i;
+          if (fl.def[i].z >= thr_f) return i;
         return nd;
       };
       // a stashed chunk comes from LDS, converted already; the others from
@@ -1770,8 +1817,8 @@ __global__ __launch_bounds__(NT) void smp_row(SmpArgs A) {
         ia = ic;
         ib = id;
       }
-      __syncthreads();  // the deferred chunks' appends are in LDS
     }
+    if (nd) __syncthreads();  // the deferred chunks' appends are in the buffer
   }
 
   // ---- segments: hand the candidates to the row's last block -------------
