@@ -381,6 +381,9 @@ int yskn_smp_validate_params_f64(const yskn_smp_params_f64* params, int32_t voca
  *                  (output_head_sampler.rs:221-228)
  *   fn 13: version-2 uniform (seed, position) u64 pairs -> binary64 (:196-197)
  *   fn 14: mix64   u64 -> u64 (:214-219)
+ *   fn 8:  serial binary64 prefix sums S_j = (..(w_0 + w_1) + ..) + w_j of n
+ *          weights (w_0 = 1 >= w_j >= 0), as the tail computes them in
+ *          parallel (output_head_sampler.rs:157-175)
  *   fn 6:  rsqrt   binary32 bits base + i -> binary32 bits (portable_math.rs:108-111)
  *   fn 7:  sqrt_rn binary32 bits base + i -> binary32 bits (portable_math.rs:61-106)
  * n in 1..2^28. Returns 0 or a negative status. */

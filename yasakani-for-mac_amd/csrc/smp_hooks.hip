@@ -4,12 +4,13 @@
 // given in host memory, so that its binary64/binary32 results can be compared
 // bit for bit with the CPU restatement. It is the counterpart of the
 // reference's yskn_pm_test (src/pm_test.cu:30-52; fn 10 = exp_d, fn 11 =
-// log_d there as here). Not on the sampling path: it allocates, copies and
-// synchronises.
+// log_d there as here), and the tail's exact prefix-sum scan (fn 8). Not on
+// the sampling path: it allocates, copies and synchronises.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
 #include "../../include/yskn_smp.h"
+#include "smp_internal.hpp"
 #include "smp_math.hpp"
 
 namespace yskn {
@@ -48,6 +49,7 @@ int words_in(int fn) {
     case 10: case 11: case 14: return 1;
     case 12: return 3;
     case 13: return 2;
+    case 8: return 1;
     case 6: case 7: return 0;
     default: return -1;
   }
@@ -61,7 +63,7 @@ extern "C" int yskn_smp_pm_test(int32_t fn, uint64_t base, const void* host_in, 
   const int win = words_in(fn);
   if (win < 0 || n <= 0 || n > (1ll << 28) || !host_out || (win > 0 && !host_in)) return YSKN_SMP_EINVAL;
   const size_t in_bytes = (size_t)n * (size_t)win * 8u;
-  const size_t out_bytes = (size_t)n * (fn >= 10 ? 8u : 4u);
+  const size_t out_bytes = (size_t)n * (fn >= 8 ? 8u : 4u);
   void* d = nullptr;
   hipError_t e = hipMalloc(&d, in_bytes + out_bytes + 16);
   if (e != hipSuccess) return YSKN_SMP_EDEVICE;
@@ -69,9 +71,13 @@ extern "C" int yskn_smp_pm_test(int32_t fn, uint64_t base, const void* host_in, 
   void* dout = (char*)d + in_bytes;
   if (win > 0) e = hipMemcpy(din, host_in, in_bytes, hipMemcpyHostToDevice);
   if (e == hipSuccess) {
-    hipLaunchKernelGGL(pm_test_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, nullptr, fn, base, din,
-                       dout, n);
-    e = hipGetLastError();
+    if (fn == 8) {
+      e = launch_prefix_test((const double*)din, (double*)dout, n, nullptr);
+    } else {
+      hipLaunchKernelGGL(pm_test_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, nullptr, fn, base, din,
+                         dout, n);
+      e = hipGetLastError();
+    }
   }
   if (e == hipSuccess) e = hipMemcpy(host_out, dout, out_bytes, hipMemcpyDeviceToHost);
   const hipError_t f = hipFree(d);

@@ -225,6 +225,9 @@ struct DraftChooseArgs {
 // Host-side launchers (smp_kernels.hip, smp_draft.hip).
 hipError_t launch_sample(const SmpArgs& a, int dtype, bool vec, bool pen, hipStream_t st);
 hipError_t launch_penalty_prep(const PenArgs& a, hipStream_t st);
+// Test hook: the exact serial prefix sums of c binary64 weights (w[0] = 1 >=
+// w[j] >= 0) by the block-parallel scan the tail uses; one block.
+hipError_t launch_prefix_test(const double* w, double* S, int64_t c, hipStream_t st);
 hipError_t launch_draft_shortlist(const DraftShortlistArgs& a, hipStream_t st);
 hipError_t launch_draft_top16(const DraftTop16Args& a, hipStream_t st);
 hipError_t launch_draft_choose(const DraftChooseArgs& a, hipStream_t st);

@@ -422,20 +422,224 @@ __device__ __forceinline__ uint64_t position_of(const SmpArgs& A, int row, int d
 }
 
 // ---------------------------------------------------------------------------
+// Exact serial binary64 prefix sums, in parallel.
+//
+// The reference sums the candidates' weights serially in candidate order
+// (output_head_sampler.rs:157-175): S_j = (..(w_0 + w_1) + ..) + w_j, each
+// add rounded to nearest-even. Here w_0 = 1 >= w_j >= 0, so S_j >= 1 and
+// every w_j <= S_{j-1}. While the sum stays in one binade [2^e, 2^(e+1)),
+// each add rounds to the grid of that binade's unit u = 2^(e-52): w_j adds
+// round(w_j / u) units, exactly, and depends on the running sum only when
+// w_j / u = q + 1/2 is a tie, which goes to the even unit count (a function
+// of the sum's parity). A tile of weights is therefore a composition of
+// functions of one parity bit, scanned across the block; the first element
+// whose sum leaves the binade is added with a real binary64 add, which
+// starts the next binade (an add can cross at most one, since w_j <= S).
+// ---------------------------------------------------------------------------
+struct PFun {
+  uint64_t d0, d1;  // units added to a running sum of even / odd unit count
+  uint32_t p;       // bit b: parity of the result from input parity b
+};
+__device__ __forceinline__ PFun pf_identity() { return PFun{0ull, 0ull, 2u}; }
+// `a` first, then `b`
+__device__ __forceinline__ PFun pf_then(const PFun& a, const PFun& b) {
+  const uint32_t a0 = a.p & 1u, a1 = (a.p >> 1) & 1u;
+  PFun r;
+  r.d0 = a.d0 + (a0 ? b.d1 : b.d0);
+  r.d1 = a.d1 + (a1 ? b.d1 : b.d0);
+  const uint32_t b0 = b.p & 1u, b1 = (b.p >> 1) & 1u;
+  r.p = (a0 ? b1 : b0) | ((a1 ? b1 : b0) << 1);
+  return r;
+}
+// the add of a weight worth x = w / u units (x >= 0, exact)
+__device__ __forceinline__ PFun pf_weight(double x) {
+  const double q = floor(x);  // exact, as is x - q
+  const double f = x - q;
+  const uint64_t qi = (uint64_t)q;
+  PFun r;
+  if (f == 0.5) {
+    // s + q + 1/2 rounds to whichever of s + q, s + q + 1 is even
+    r.d0 = qi + (qi & 1ull);
+    r.d1 = qi + ((qi + 1ull) & 1ull);
+    r.p = 0u;
+  } else {
+    const uint64_t d = qi + (f > 0.5 ? 1ull : 0ull);
+    r.d0 = d;
+    r.d1 = d;
+    const uint32_t b = (uint32_t)(d & 1ull);
+    r.p = b | ((b ^ 1u) << 1);
+  }
+  return r;
+}
+__device__ __forceinline__ PFun pf_shfl_up(const PFun& x, int o) {
+  PFun y;
+  y.d0 = (uint64_t)__shfl_up((unsigned long long)x.d0, o);
+  y.d1 = (uint64_t)__shfl_up((unsigned long long)x.d1, o);
+  y.p = (uint32_t)__shfl_up((int)x.p, o);
+  return y;
+}
+
+struct PScanShared {
+  PFun wave[NW];
+  double s;     // the sum before the next element
+  int64_t j0;   // the next element
+  int64_t jc;   // the first element of the tile whose sum leaves the binade
+};
+
+// S[j] for j < c (S may alias w: every element is read before it is
+// written). Block-wide.
+__device__ void exact_prefix(const double* w, double* S, int64_t c, PScanShared* ps) {
+  constexpr int PT = 8;  // elements per thread and tile
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  if (tid == 0) {
+    const double s0 = w[0];
+    S[0] = s0;
+    ps->s = s0;
+    ps->j0 = 1;
+  }
+  __syncthreads();
+  for (;;) {
+    const int64_t j0 = ps->j0;
+    if (j0 >= c) break;  // (block-uniform)
+    const double s = ps->s;
+    const uint64_t sb = (uint64_t)__double_as_longlong(s);
+    const int E = (int)(sb >> 52);  // biased exponent: s >= 1 is normal
+    const uint64_t su = (sb & 0x000fffffffffffffull) | 0x0010000000000000ull;  // s / u
+    const int sh = 1075 - E;                                                    // w / u = w * 2^sh
+    const double u = __longlong_as_double((long long)((uint64_t)(E - 52) << 52));
+    const int64_t jb = j0 + (int64_t)tid * PT;
+    const int64_t je = j0 + (int64_t)NT * PT < c ? j0 + (int64_t)NT * PT : c;  // tile end
+    __syncthreads();  // ps->s and ps->j0 read
+    if (tid == 0) ps->jc = INT64_MAX;
+    PFun f[PT];
+    double wv[PT];
+    PFun mine = pf_identity();
+#pragma unroll
+    for (int q = 0; q < PT; ++q) {
+      const int64_t j = jb + q;
+      wv[q] = j < je ? w[j] : 0.0;
+      f[q] = j < je ? pf_weight(ldexp(wv[q], sh)) : pf_identity();
+      mine = pf_then(mine, f[q]);
+    }
+    // exclusive scan of the threads' functions, in thread order
+    PFun inc = mine;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const PFun y = pf_shfl_up(inc, o);
+      if (lane >= o) inc = pf_then(y, inc);
+    }
+    PFun before = pf_shfl_up(inc, 1);
+    if (lane == 0) before = pf_identity();
+    if (lane == 63) ps->wave[wave] = inc;
+    __syncthreads();
+    PFun pre = pf_identity();
+    for (int k = 0; k < wave; ++k) pre = pf_then(pre, ps->wave[k]);
+    pre = pf_then(pre, before);
+    // this thread's sums in units of u; the first that leaves the binade
+    uint32_t p = (uint32_t)(su & 1ull);
+    uint64_t acc = p ? pre.d1 : pre.d0;
+    p = (pre.p >> p) & 1u;
+    uint64_t accs[PT];
+    int64_t my_jc = INT64_MAX;
+    double s_prev_c = 0.0, w_c = 0.0, s_last = 0.0;
+#pragma unroll
+    for (int q = 0; q < PT; ++q) {
+      const int64_t j = jb + q;
+      const uint64_t a0 = acc;
+      if (j < je) {
+        acc += p ? f[q].d1 : f[q].d0;
+        p = (f[q].p >> p) & 1u;
+        if (my_jc == INT64_MAX && su + acc >= (1ull << 53)) {
+          my_jc = j;
+          s_prev_c = (double)(su + a0) * u;
+          w_c = wv[q];
+        }
+        if (j == je - 1) s_last = (double)(su + acc) * u;
+      }
+      accs[q] = acc;
+    }
+    if (my_jc != INT64_MAX) atomicMin((unsigned long long*)&ps->jc, (unsigned long long)my_jc);
+    __syncthreads();
+    const int64_t jc = ps->jc;
+    const int64_t jw = jc < je ? jc : je;  // elements below jw stay in the binade
+#pragma unroll
+    for (int q = 0; q < PT; ++q) {
+      const int64_t j = jb + q;
+      if (j < jw) S[j] = (double)(su + accs[q]) * u;
+    }
+    if (jc < je) {
+      if (my_jc == jc) {
+        const double sn = s_prev_c + w_c;  // the serial add itself
+        S[jc] = sn;
+        ps->s = sn;
+        ps->j0 = jc + 1;
+      }
+    } else if (je - 1 >= jb && je - 1 < jb + PT) {
+      ps->s = s_last;
+      ps->j0 = je;
+    }
+    __syncthreads();
+  }
+}
+
+// First j in [lo, hi) with S[j] >= t (strict: S[j] > t), or hi; S is
+// non-decreasing. One wave, 64 probes per round. Every lane returns it.
+__device__ __forceinline__ int64_t first_reaching(const double* S, int64_t lo, int64_t hi, double t, bool strict) {
+  const int lane = threadIdx.x & 63;
+  while (hi - lo > 64) {
+    const int64_t step = (hi - lo + 63) / 64;
+    int64_t idx = lo + (int64_t)(lane + 1) * step - 1;
+    if (idx > hi - 1) idx = hi - 1;
+    const double v = S[idx];
+    const uint64_t m = __ballot(strict ? v > t : v >= t);
+    if (!m) return hi;
+    const int64_t L = (int64_t)__builtin_ctzll(m);
+    const int64_t nlo = lo + L * step;
+    const int64_t nhi = lo + (L + 1) * step;
+    lo = nlo;
+    hi = nhi < hi ? nhi : hi;
+  }
+  const int64_t idx = lo + lane;
+  const bool in = idx < hi;
+  const double v = in ? S[idx] : 0.0;
+  const uint64_t m = __ballot(in && (strict ? v > t : v >= t));
+  return m ? lo + (int64_t)__builtin_ctzll(m) : hi;
+}
+// First j in [lo, hi) with w[j] < t, or hi; w is non-increasing.
+__device__ __forceinline__ int64_t first_below(const double* w, int64_t lo, int64_t hi, double t) {
+  const int lane = threadIdx.x & 63;
+  while (hi - lo > 64) {
+    const int64_t step = (hi - lo + 63) / 64;
+    int64_t idx = lo + (int64_t)(lane + 1) * step - 1;
+    if (idx > hi - 1) idx = hi - 1;
+    const uint64_t m = __ballot(w[idx] < t);
+    if (!m) return hi;
+    const int64_t L = (int64_t)__builtin_ctzll(m);
+    const int64_t nhi = lo + (L + 1) * step;
+    lo = lo + L * step;
+    hi = nhi < hi ? nhi : hi;
+  }
+  const int64_t idx = lo + lane;
+  const bool in = idx < hi;
+  const uint64_t m = __ballot(in && w[in ? idx : lo] < t);
+  return m ? lo + (int64_t)__builtin_ctzll(m) : hi;
+}
+
+// ---------------------------------------------------------------------------
 // Truncation and draw on the first c sorted candidates (output_head_sampler.rs
-// :136-212). cand/w are generic pointers (LDS or global scratch).
+// :136-212). cand/w are generic pointers (LDS or global scratch); w is
+// overwritten with the prefix sums.
 // ---------------------------------------------------------------------------
 struct TailShared {
-  uint32_t retained;
+  int64_t retained;
   double mass;  // serial binary64 sum of the retained weights (version 2)
-  double best;
-  int pick;
+  PScanShared scan;
 };
 
 __device__ __forceinline__ void sample_tail(const SmpArgs& A, const DevParams& P, int row, const uint64_t* cand,
                             double* w, int64_t c, TailShared* ts, double* redd, int* redi,
                             uint64_t* redu) {
-  const int tid = threadIdx.x;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const double T = P.temperature;
   const float v0 = key2f(pk_key(cand[0]));
   // weights: widen, subtract, divide, exp_d -- in candidate order
@@ -444,88 +648,82 @@ __device__ __forceinline__ void sample_tail(const SmpArgs& A, const DevParams& P
     w[j] = exp_d(z);
   }
   __syncthreads();
-  if (tid == 0) {
-    double total = 0.0;
-    for (int64_t j = 0; j < c; ++j) total = total + w[j];
-    int64_t n = c;
-    double prefix = 0.0;
-    const double thr = P.top_p * total;
-    for (int64_t j = 0; j < c; ++j) {
-      prefix = prefix + w[j];
-      if (prefix >= thr) {
-        n = j + 1;
-        break;
-      }
+  // min-p relative to w_0 = 1: the first j >= 1 with w_j < min_p ends the
+  // kept prefix (the weights do not increase along the candidates)
+  if (wave == 0) {
+    const int64_t m = P.min_p > 0.0 ? first_below(w, 1, c, P.min_p) : c;
+    if (lane == 0) ts->retained = m;
+  }
+  __syncthreads();
+  // the serial prefix sums, exactly
+  exact_prefix(w, w, c, &ts->scan);
+  if (wave == 0) {
+    const double total = w[c - 1];
+    // top-p: the first n with prefix_{n-1} >= top_p * total (:160-166)
+    const int64_t n = first_reaching(w, 0, c, P.top_p * total, false);
+    int64_t r = n < c ? n + 1 : c;
+    const int64_t m = ts->retained;
+    if (m < r) r = m;
+    if (lane == 0) {
+      ts->retained = r;
+      ts->mass = w[r - 1];  // the retained mass: the same serial sum (:191)
     }
-    if (P.min_p > 0.0) {
-      int64_t m = 1;
-      while (m < n && w[m] >= P.min_p) ++m;
-      n = m;
-    }
-    double mass = 0.0;
-    if (P.version != YSKN_V3) {
-      for (int64_t j = 0; j < n; ++j) mass = mass + w[j];
-    }
-    ts->retained = (uint32_t)n;
-    ts->mass = mass;
   }
   __syncthreads();
   const int64_t r = ts->retained;
   const int nd = A.mode == MODE_VERIFY ? 1 : A.n_draws;
-  if (P.version == YSKN_V3 && nd == 1) {
-    // one draw: candidates in parallel, argmax of z + g with the earliest
-    // candidate winning ties (strict > in candidate order)
-    const uint64_t pk = position_key(P.seed, position_of(A, row, 0));
-    double best = -__builtin_inf();
-    int64_t bj = r - 1;
-    for (int64_t j = tid; j < r; j += NT) {
-      const uint64_t cj = cand[j];
-      const double z = ((double)key2f(pk_key(cj)) - (double)v0) / T;
-      const double s = z + gumbel_from_key(pk, pk_id(cj));
-      if (s > best || (s == best && j < bj)) {
-        best = s;
-        bj = j;
-      }
-    }
-    // reduce (best desc, index asc) across the block
-    const int lane = tid & 63, wave = tid >> 6;
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) {
-      const double ob = __shfl_xor(best, o);
-      const int64_t oj = __shfl_xor((long long)bj, o);
-      if (ob > best || (ob == best && oj < bj)) {
-        best = ob;
-        bj = oj;
-      }
-    }
-    __syncthreads();
-    if (lane == 0) {
-      redd[wave] = best;
-      redi[wave] = (int)bj;
-    }
-    __syncthreads();
-    if (tid == 0) {
-      double b = redd[0];
-      int jj = redi[0];
-      for (int q = 1; q < NW; ++q) {
-        if (redd[q] > b || (redd[q] == b && redi[q] < jj)) {
-          b = redd[q];
-          jj = redi[q];
+  if (P.version == YSKN_V3 && (nd == 1 || r > 64)) {
+    // each draw over the candidates in parallel: argmax of z + g with the
+    // earliest candidate winning ties (strict > in candidate order)
+    for (int d = 0; d < nd; ++d) {
+      const uint64_t pk = position_key(P.seed, position_of(A, row, d));
+      double best = -__builtin_inf();
+      int64_t bj = r - 1;
+      for (int64_t j = tid; j < r; j += NT) {
+        const uint64_t cj = cand[j];
+        const double z = ((double)key2f(pk_key(cj)) - (double)v0) / T;
+        const double s = z + gumbel_from_key(pk, pk_id(cj));
+        if (s > best || (s == best && j < bj)) {
+          best = s;
+          bj = j;
         }
       }
-      const uint32_t id = pk_id(cand[jj]);
-      A.out_ids[(int64_t)row * A.n_draws] = id;
+#pragma unroll
+      for (int o = 32; o > 0; o >>= 1) {
+        const double ob = __shfl_xor(best, o);
+        const int64_t oj = __shfl_xor((long long)bj, o);
+        if (ob > best || (ob == best && oj < bj)) {
+          best = ob;
+          bj = oj;
+        }
+      }
+      __syncthreads();
+      if (lane == 0) {
+        redd[wave] = best;
+        redu[wave] = (uint64_t)bj;
+      }
+      __syncthreads();
+      if (tid == 0) {
+        double b = redd[0];
+        int64_t jj = (int64_t)redu[0];
+        for (int q = 1; q < NW; ++q) {
+          if (redd[q] > b || (redd[q] == b && (int64_t)redu[q] < jj)) {
+            b = redd[q];
+            jj = (int64_t)redu[q];
+          }
+        }
+        A.out_ids[(int64_t)row * A.n_draws + d] = pk_id(cand[jj]);
+      }
     }
     __syncthreads();
     return;
   }
-  // several draws (or version 2): one thread per draw, serial over candidates
-  for (int d = tid; d < nd; d += NT) {
-    const uint64_t pos = position_of(A, row, d);
-    int64_t pick = r - 1;
-    if (P.version == YSKN_V3) {
-      const uint64_t pk = position_key(P.seed, pos);
+  if (P.version == YSKN_V3) {
+    // several draws over at most 64 candidates: one thread per draw
+    for (int d = tid; d < nd; d += NT) {
+      const uint64_t pk = position_key(P.seed, position_of(A, row, d));
       double best = -__builtin_inf();
+      int64_t pick = r - 1;
       for (int64_t j = 0; j < r; ++j) {
         const uint64_t cj = cand[j];
         const double z = ((double)key2f(pk_key(cj)) - (double)v0) / T;
@@ -535,19 +733,17 @@ __device__ __forceinline__ void sample_tail(const SmpArgs& A, const DevParams& P
           pick = j;
         }
       }
-    } else {
-      const double u = uniform_v2(P.seed, pos);
-      const double thr = u * ts->mass;
-      double prefix = 0.0;
-      for (int64_t j = 0; j < r; ++j) {
-        prefix = prefix + w[j];
-        if (thr < prefix) {
-          pick = j;
-          break;
-        }
-      }
+      A.out_ids[(int64_t)row * A.n_draws + d] = pk_id(cand[pick]);
     }
-    A.out_ids[(int64_t)row * A.n_draws + d] = pk_id(cand[pick]);
+    __syncthreads();
+    return;
+  }
+  // version 2: draw d picks the first j with u_d * mass < prefix_j
+  // (:196-207), by a search of the prefix sums; one wave per draw
+  for (int d = wave; d < nd; d += NW) {
+    const double t = uniform_v2(P.seed, position_of(A, row, d)) * ts->mass;
+    const int64_t j = first_reaching(w, 0, r, t, true);
+    if (lane == 0) A.out_ids[(int64_t)row * A.n_draws + d] = pk_id(cand[j < r ? j : r - 1]);
   }
   __syncthreads();
 }
@@ -2335,6 +2531,16 @@ hipError_t launch_sample(const SmpArgs& a, int dtype, bool vec, bool pen, hipStr
   }
   if (vec) return pen ? launch_t<1, true, true>(a, st) : launch_t<1, true, false>(a, st);
   return pen ? launch_t<1, false, true>(a, st) : launch_t<1, false, false>(a, st);
+}
+
+__global__ __launch_bounds__(NT) void smp_prefix_test(const double* w, double* S, int64_t c) {
+  __shared__ PScanShared ps;
+  exact_prefix(w, S, c, &ps);
+}
+
+hipError_t launch_prefix_test(const double* w, double* S, int64_t c, hipStream_t st) {
+  hipLaunchKernelGGL(smp_prefix_test, dim3(1), dim3(NT), 0, st, w, S, c);
+  return hipGetLastError();
 }
 
 hipError_t launch_penalty_prep(const PenArgs& a, hipStream_t st) {
