@@ -217,8 +217,11 @@ bool any_penalty(yskn_smp_handle h, int32_t rows) {
 }
 
 // Segments per row. A block streams one segment; small batches split rows so
-// that the call spreads over the CUs (about one 2,048-logit chunk per wave,
-// about 512 blocks in all); from 192 rows on, each row is one block.
+// that the call spreads over the CUs: about one 2,048-logit chunk per wave,
+// and at most 256 blocks in all, one per CU (a block's LDS fills a CU), so
+// that every block is resident from the start: a block queued behind a CU
+// held by a long finish (the dense path) would hold back its row. From 192
+// rows on, each row is one block.
 // YSKN_SMP_SEGMENTS=n (1..32) fixes the count for measurements.
 int segments_for(int32_t rows, int32_t vocab) {
   static const int forced = [] {
@@ -233,7 +236,7 @@ int segments_for(int32_t rows, int32_t vocab) {
     s = 1;
   } else {
     const int by_chunks = (nch + NW - 1) / NW;
-    const int by_blocks = (512 + rows - 1) / rows;
+    const int by_blocks = 256 / rows > 1 ? 256 / rows : 1;
     s = by_chunks < by_blocks ? by_chunks : by_blocks;
   }
   if (s > SEG_MAX) s = SEG_MAX;

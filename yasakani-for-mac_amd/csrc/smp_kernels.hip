@@ -511,15 +511,13 @@ __device__ void exact_prefix(const double* w, double* S, int64_t c, PScanShared*
     const int64_t je = j0 + (int64_t)NT * PT < c ? j0 + (int64_t)NT * PT : c;  // tile end
     __syncthreads();  // ps->s and ps->j0 read
     if (tid == 0) ps->jc = INT64_MAX;
-    PFun f[PT];
-    double wv[PT];
+    double wv[PT];  // (the per-element functions are formed again where needed)
     PFun mine = pf_identity();
 #pragma unroll
     for (int q = 0; q < PT; ++q) {
       const int64_t j = jb + q;
       wv[q] = j < je ? w[j] : 0.0;
-      f[q] = j < je ? pf_weight(ldexp(wv[q], sh)) : pf_identity();
-      mine = pf_then(mine, f[q]);
+      if (j < je) mine = pf_then(mine, pf_weight(ldexp(wv[q], sh)));
     }
     // exclusive scan of the threads' functions, in thread order
     PFun inc = mine;
@@ -536,19 +534,21 @@ __device__ void exact_prefix(const double* w, double* S, int64_t c, PScanShared*
     for (int k = 0; k < wave; ++k) pre = pf_then(pre, ps->wave[k]);
     pre = pf_then(pre, before);
     // this thread's sums in units of u; the first that leaves the binade
-    uint32_t p = (uint32_t)(su & 1ull);
-    uint64_t acc = p ? pre.d1 : pre.d0;
-    p = (pre.p >> p) & 1u;
-    uint64_t accs[PT];
+    const uint32_t p0 = (uint32_t)(su & 1ull);
+    const uint64_t acc0 = p0 ? pre.d1 : pre.d0;
+    const uint32_t pp0 = (pre.p >> p0) & 1u;
+    uint32_t p = pp0;
+    uint64_t acc = acc0;
     int64_t my_jc = INT64_MAX;
     double s_prev_c = 0.0, w_c = 0.0, s_last = 0.0;
 #pragma unroll
     for (int q = 0; q < PT; ++q) {
       const int64_t j = jb + q;
-      const uint64_t a0 = acc;
       if (j < je) {
-        acc += p ? f[q].d1 : f[q].d0;
-        p = (f[q].p >> p) & 1u;
+        const uint64_t a0 = acc;
+        const PFun f = pf_weight(ldexp(wv[q], sh));
+        acc += p ? f.d1 : f.d0;
+        p = (f.p >> p) & 1u;
         if (my_jc == INT64_MAX && su + acc >= (1ull << 53)) {
           my_jc = j;
           s_prev_c = (double)(su + a0) * u;
@@ -556,16 +556,22 @@ __device__ void exact_prefix(const double* w, double* S, int64_t c, PScanShared*
         }
         if (j == je - 1) s_last = (double)(su + acc) * u;
       }
-      accs[q] = acc;
     }
     if (my_jc != INT64_MAX) atomicMin((unsigned long long*)&ps->jc, (unsigned long long)my_jc);
     __syncthreads();
     const int64_t jc = ps->jc;
     const int64_t jw = jc < je ? jc : je;  // elements below jw stay in the binade
+    p = pp0;
+    acc = acc0;
 #pragma unroll
     for (int q = 0; q < PT; ++q) {
       const int64_t j = jb + q;
-      if (j < jw) S[j] = (double)(su + accs[q]) * u;
+      if (j < jw) {
+        const PFun f = pf_weight(ldexp(wv[q], sh));
+        acc += p ? f.d1 : f.d0;
+        p = (f.p >> p) & 1u;
+        S[j] = (double)(su + acc) * u;
+      }
     }
     if (jc < je) {
       if (my_jc == jc) {
@@ -645,7 +651,7 @@ __device__ __forceinline__ void sample_tail(const SmpArgs& A, const DevParams& P
   // weights: widen, subtract, divide, exp_d -- in candidate order
   for (int64_t j = tid; j < c; j += NT) {
     const double z = ((double)key2f(pk_key(cand[j])) - (double)v0) / T;
-    w[j] = exp_d(z);
+    w[j] = exp_d_inline(z);
   }
   __syncthreads();
   // min-p relative to w_0 = 1: the first j >= 1 with w_j < min_p ends the
@@ -842,6 +848,29 @@ __device__ __forceinline__ void sample_tail_wave(const SmpArgs& A, const DevPara
 // The exact need-th largest key of the row (1 <= need <= V): four 8-bit
 // radix passes from the top over the whole row. hist: 256 LDS words, bc: 2.
 // Block-wide; every thread returns the key.
+// Histogram increment of an 8-bit `bin` for the valid lanes of a wave:
+// lanes with equal bins are found with one ballot per bit and the lowest of
+// them adds their number (one LDS atomic per distinct bin, not per lane:
+// concentrated keys would otherwise serialise on a few counters).
+__device__ __forceinline__ uint64_t bin_peers(uint32_t bin, bool valid) {
+  uint64_t peers = __ballot(valid);
+#pragma unroll
+  for (int b = 0; b < 8; ++b) {
+    const bool bit = (bin >> b) & 1u;
+    const uint64_t bal = __ballot(bit);
+    peers &= bit ? bal : ~bal;
+  }
+  return peers;
+}
+__device__ __forceinline__ void hist_add8(uint32_t* hist, uint32_t bin, bool valid) {
+  const int lane = threadIdx.x & 63;
+  const uint64_t peers = bin_peers(bin, valid);
+  if (valid && (peers & ((1ull << lane) - 1ull)) == 0ull) atomicAdd(&hist[bin], (uint32_t)__popcll(peers));
+}
+
+// The exact need-th largest key of the row (1 <= need <= V): four 8-bit
+// radix passes from the top over the whole row. hist: 256 LDS words, bc: 2.
+// Block-wide; every thread returns the key.
 template <int DT, bool PEN>
 __device__ __forceinline__ uint32_t radix_kth_key(const RowCtx& rc, int V, int64_t need_in, uint32_t* hist,
                                                   uint32_t* bc) {
@@ -852,9 +881,10 @@ __device__ __forceinline__ uint32_t radix_kth_key(const RowCtx& rc, int V, int64
     const int shift = 24 - 8 * pass;
     for (int i = tid; i < 256; i += NT) hist[i] = 0;
     __syncthreads();
-    for (int64_t i = tid; i < V; i += NT) {
-      const uint32_t k = f2key(value_bits<DT, PEN>(rc, i));
-      if ((k & mask) == prefix) atomicAdd(&hist[(k >> shift) & 255u], 1u);
+    for (int64_t i0 = 0; i0 < V; i0 += NT) {
+      const int64_t i = i0 + tid;
+      const uint32_t k = i < V ? f2key(value_bits<DT, PEN>(rc, i)) : 0u;
+      hist_add8(hist, (k >> shift) & 255u, i < V && (k & mask) == prefix);
     }
     __syncthreads();
     if (tid == 0) {
@@ -881,94 +911,209 @@ __device__ __forceinline__ uint32_t radix_kth_key(const RowCtx& rc, int V, int64
   return prefix;
 }
 
+// Order-preserving compaction of the row's elements with key >= theta
+// (theta >= 1) into da as packed (key, id) entries, ids ascending. Tiles of
+// NT * 8 elements read coalesced: element (q, t) is tile + q * NT + t, and
+// its rank counts the kept elements of rows q' < q, of the waves before t's
+// in row q and of the lanes below it. lds: 65 words. Returns the count.
+template <int DT, bool PEN>
+__device__ int64_t dense_compact(const RowCtx& rc, int V, uint32_t theta, uint64_t* da, uint32_t* lds) {
+  constexpr int PER = 8;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  uint32_t* cnt = lds;              // [PER][NW] counts, then offsets
+  uint32_t* tot = lds + PER * NW;
+  const uint64_t below = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+  int64_t n = 0;
+  for (int64_t base = 0; base < V; base += (int64_t)NT * PER) {
+    uint32_t keys[PER];
+    uint64_t m[PER];
+#pragma unroll
+    for (int q = 0; q < PER; ++q) {
+      const int64_t i = base + (int64_t)q * NT + tid;
+      keys[q] = i < V ? f2key(value_bits<DT, PEN>(rc, i)) : 0u;
+    }
+#pragma unroll
+    for (int q = 0; q < PER; ++q) {
+      m[q] = __ballot(keys[q] >= theta);
+      if (lane == 0) cnt[q * NW + wave] = (uint32_t)__popcll(m[q]);
+    }
+    __syncthreads();
+    if (wave == 0) {
+      static_assert(PER * NW == 64, "one (row, wave) count per lane");
+      const uint32_t c0 = cnt[lane];
+      const uint32_t inc = (uint32_t)wave_incl_scan((int)c0, lane);
+      cnt[lane] = inc - c0;
+      if (lane == 63) *tot = inc;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int q = 0; q < PER; ++q) {
+      if (keys[q] >= theta)
+        da[n + cnt[q * NW + wave] + (uint32_t)__popcll(m[q] & below)] =
+            pack(keys[q], (uint32_t)(base + (int64_t)q * NT + tid));
+    }
+    n += *tot;
+    __syncthreads();
+  }
+  return n;
+}
+
+// Stable sort of n packed (key, id) entries by key, descending (equal keys
+// keep their order): LSD passes on the key bytes, digit 255 - byte, between
+// a and b; a pass whose digit is the same for every entry is skipped; the
+// result ends in a. One pass over the entries first counts all four digit
+// histograms (plain LDS atomics: no order is needed there). A pass takes
+// tiles of NT * 8 entries: wave w holds the
+// tile's entries w * 512 + 64 q + lane (q < 8) and counts their digits;
+// each entry's place in the tile, in (digit, wave, slot, lane) order, puts
+// it in the LDS tile buffer, which is then written out in order: a digit's
+// entries of the tile are one contiguous run of the destination.
+// lds: 5,888 words; sbuf: NT * 8 entries. Block-wide.
+__device__ void lsd_sort_desc(uint64_t* a, uint64_t* b, int64_t n, uint32_t* lds, uint64_t* sbuf) {
+  constexpr int PER = 8;
+  constexpr int64_t TILE = (int64_t)NT * PER;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  uint32_t* gb = lds;                      // [4][256] digit counts, then running bases
+  uint32_t* wc = lds + 1024;               // [NW][256] per-wave digit counts / cursors
+  uint32_t* wo = lds + 1024 + NW * 256;    // [256][NW] per-wave offsets within a digit
+  uint32_t* ts = lds + 1024 + 2 * NW * 256;        // [256] the tile's digit starts
+  uint32_t* tc = lds + 1024 + 2 * NW * 256 + 256;  // [256] the tile's digit counts
+  uint32_t* skip = lds + 1024 + 2 * NW * 256 + 512;  // [4] one digit only
+  for (int i = tid; i < 1024; i += NT) gb[i] = 0u;
+  __syncthreads();
+  for (int64_t i = tid; i < n; i += NT) {
+    const uint32_t key = (uint32_t)(a[i] >> 32);
+#pragma unroll
+    for (int p = 0; p < 4; ++p) atomicAdd(&gb[p * 256 + (255u - ((key >> (8 * p)) & 255u))], 1u);
+  }
+  __syncthreads();
+  if (wave < 4) {
+    // exclusive scan of pass `wave`'s 256 counts, four per lane
+    uint32_t c[4], loc = 0u;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      c[q] = gb[wave * 256 + lane * 4 + q];
+      loc += c[q];
+    }
+    const bool one = __ballot(c[0] == (uint32_t)n || c[1] == (uint32_t)n || c[2] == (uint32_t)n ||
+                              c[3] == (uint32_t)n) != 0ull;
+    const uint32_t inc = (uint32_t)wave_incl_scan((int)loc, lane);
+    uint32_t run = inc - loc;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      gb[wave * 256 + lane * 4 + q] = run;
+      run += c[q];
+    }
+    if (lane == 0) skip[wave] = one ? 1u : 0u;
+  }
+  __syncthreads();
+  const uint64_t below = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+  uint64_t* src = a;
+  uint64_t* dst = b;
+  for (int p = 0; p < 4; ++p) {
+    if (skip[p]) continue;  // (block-uniform)
+    const int shift = 32 + 8 * p;
+    for (int64_t t0 = 0; t0 < n; t0 += TILE) {
+      const int64_t tn = n - t0 < TILE ? n - t0 : TILE;
+      uint64_t e[PER];
+      uint32_t d[PER];
+      uint64_t pm[PER];
+      const int64_t wb = t0 + (int64_t)wave * 64 * PER;
+#pragma unroll
+      for (int q = 0; q < PER; ++q) {
+        const int64_t i = wb + q * 64 + lane;
+        e[q] = i < n ? src[i] : 0ull;
+      }
+      for (int i = lane; i < 256; i += 64) wc[wave * 256 + i] = 0u;
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+#pragma unroll
+      for (int q = 0; q < PER; ++q) {
+        const bool v = wb + q * 64 + lane < n;
+        d[q] = 255u - (uint32_t)((e[q] >> shift) & 255u);
+        pm[q] = bin_peers(d[q], v);
+        if (v && (pm[q] & below) == 0ull) atomicAdd(&wc[wave * 256 + d[q]], (uint32_t)__popcll(pm[q]));
+      }
+      __syncthreads();
+      if (wave == 0) {
+        // digits 4 lane .. 4 lane + 3: offsets of the waves within each
+        // digit, the tile's digit counts and (scanned) starts
+        uint32_t loc = 0u;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          const int dd = lane * 4 + k;
+          uint32_t run = 0u;
+#pragma unroll
+          for (int w = 0; w < NW; ++w) {
+            const uint32_t c = wc[w * 256 + dd];
+            wo[dd * NW + w] = run;
+            wc[w * 256 + dd] = 0u;
+            run += c;
+          }
+          tc[dd] = run;
+          loc += run;
+        }
+        const uint32_t inc = (uint32_t)wave_incl_scan((int)loc, lane);
+        uint32_t st = inc - loc;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          ts[lane * 4 + k] = st;
+          st += tc[lane * 4 + k];
+        }
+      }
+      __syncthreads();
+#pragma unroll
+      for (int q = 0; q < PER; ++q) {
+        const bool v = wb + q * 64 + lane < n;
+        const int lead = v ? (int)__builtin_ctzll(pm[q]) : lane;
+        uint32_t old = 0u;
+        if (v && lead == lane) old = atomicAdd(&wc[wave * 256 + d[q]], (uint32_t)__popcll(pm[q]));
+        old = (uint32_t)__shfl((int)old, lead);
+        if (v) sbuf[ts[d[q]] + wo[d[q] * NW + wave] + old + (uint32_t)__popcll(pm[q] & below)] = e[q];
+      }
+      __syncthreads();
+      for (int i = tid; i < (int)tn; i += NT) {
+        const uint64_t x = sbuf[i];
+        const uint32_t dd = 255u - (uint32_t)((x >> shift) & 255u);
+        dst[gb[p * 256 + dd] + (uint32_t)i - ts[dd]] = x;
+      }
+      __syncthreads();
+      if (tid < 256) gb[p * 256 + tid] += tc[tid];
+      __syncthreads();
+    }
+    uint64_t* t = src;
+    src = dst;
+    dst = t;
+  }
+  if (src != a) {
+    for (int64_t i = tid; i < n; i += NT) a[i] = src[i];
+    __syncthreads();
+  }
+}
+
+static_assert(BUFCAP >= NT * 8, "the append buffer holds a sort tile");
+static_assert(2 * CAP >= 5888, "the candidate array holds the sort's counters");
+
+// The dense path's candidates: every element with key >= theta, sorted
+// (value desc, id asc) in dense_a. theta is the smaller of the KB-th
+// largest key and, for large-k sampling, the relevance key; when at least
+// KB elements reach the relevance key, the KB-th largest is among them and
+// needs no selection pass. lds: 5,888 words; sbuf: NT * 8 entries.
 template <int DT, bool PEN>
 __device__ __forceinline__ int64_t dense_build(const SmpArgs& A, const RowCtx& rc, int row, uint32_t theta_rel,
-                               bool need_rel, int KB, uint32_t* lds, int* redi) {
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+                                               bool need_rel, int KB, uint32_t* lds, uint64_t* sbuf) {
   const int V = A.V;
-  uint32_t* hist = lds;              // 256
-  uint32_t* dbase = lds + 256;       // 256
-  uint32_t* wcnt = lds + 512;        // NW * 256
-  uint32_t* bc = lds + 512 + NW * 256;  // broadcast words
-  // (a) exact KB-th largest key
-  const uint32_t prefix = radix_kth_key<DT, PEN>(rc, V, KB, hist, bc);
-  uint32_t theta = prefix;
-  if (need_rel && theta_rel < theta) theta = theta_rel;
-  if (theta < 1u) theta = 1u;
-  // (b) order-preserving compaction of key >= theta into dense_a
   uint64_t* da = A.dense_a + (int64_t)row * A.dense_ld;
   uint64_t* db = A.dense_b + (int64_t)row * A.dense_ld;
   int64_t n = 0;
-  for (int64_t base = 0; base < V; base += NT) {
-    const int64_t i = base + tid;
-    uint64_t p = 0;
-    int f = 0;
-    if (i < V) {
-      const uint32_t k = f2key(value_bits<DT, PEN>(rc, i));
-      if (k >= theta) {
-        f = 1;
-        p = pack(k, (uint32_t)i);
-      }
-    }
-    int tot;
-    const int off = block_excl_scan(f, redi, &tot);
-    if (f) da[n + off] = p;
-    n += tot;
+  if (need_rel) n = dense_compact<DT, PEN>(rc, V, theta_rel < 1u ? 1u : theta_rel, da, lds);
+  if (!need_rel || n < (int64_t)KB) {
+    uint32_t theta = radix_kth_key<DT, PEN>(rc, V, KB, lds, lds + 256);
+    if (need_rel && theta_rel < theta) theta = theta_rel;
+    if (theta < 1u) theta = 1u;
+    n = dense_compact<DT, PEN>(rc, V, theta, da, lds);
   }
-  __syncthreads();
-  // (c) stable LSD radix sort on the key, descending (digit = 255 - byte)
-  for (int pass = 0; pass < 4; ++pass) {
-    const int shift = 32 + 8 * pass;
-    uint64_t* src = (pass & 1) ? db : da;
-    uint64_t* dst = (pass & 1) ? da : db;
-    for (int i = tid; i < 256; i += NT) hist[i] = 0;
-    __syncthreads();
-    for (int64_t i = tid; i < n; i += NT) {
-      const uint32_t d = 255u - (uint32_t)((src[i] >> shift) & 255u);
-      atomicAdd(&hist[d], 1u);
-    }
-    __syncthreads();
-    if (tid == 0) {
-      uint32_t run = 0;
-      for (int d = 0; d < 256; ++d) {
-        dbase[d] = run;
-        run += hist[d];
-      }
-    }
-    __syncthreads();
-    for (int64_t base = 0; base < n; base += NT) {
-      const int64_t i = base + tid;
-      const bool valid = i < n;
-      const uint64_t p = valid ? src[i] : 0ull;
-      const uint32_t d = valid ? 255u - (uint32_t)((p >> shift) & 255u) : 0u;
-      for (int j = tid; j < NW * 256; j += NT) wcnt[j] = 0;
-      __syncthreads();
-      uint64_t peers = __ballot(valid);
-#pragma unroll
-      for (int b = 0; b < 8; ++b) {
-        const bool bit = (d >> b) & 1u;
-        const uint64_t bal = __ballot(bit);
-        peers &= bit ? bal : ~bal;
-      }
-      const uint64_t below = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
-      const uint32_t rank = (uint32_t)__popcll(peers & below);
-      if (valid && rank == 0) wcnt[wave * 256 + d] = (uint32_t)__popcll(peers);
-      __syncthreads();
-      if (valid) {
-        uint32_t off = dbase[d] + rank;
-        for (int q = 0; q < wave; ++q) off += wcnt[q * 256 + d];
-        dst[off] = p;
-      }
-      __syncthreads();
-      if (tid < 256) {
-        uint32_t s = 0;
-        for (int q = 0; q < NW; ++q) s += wcnt[q * 256 + tid];
-        dbase[tid] += s;
-      }
-      __syncthreads();
-    }
-  }
-  // four passes: the sorted result is back in dense_a
+  lsd_sort_desc(da, db, n, lds, sbuf);
   return n;
 }
 
@@ -2228,7 +2373,7 @@ __global__ __launch_bounds__(NT) void smp_row(SmpArgs A) {
     } else {
       const uint32_t trel = relevance_key(M, P.temperature);
       ncand = dense_build<DT, PEN>(A, rc, row, trel, plan.need_rel, plan.KB, (uint32_t*)fl.cand,
-                                   red_int);
+                                   (uint64_t*)fl.buf);
       __syncthreads();
       cand = A.dense_a + (int64_t)row * A.dense_ld;
       wbuf = A.dense_w + (int64_t)row * A.dense_ld;
