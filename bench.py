@@ -151,19 +151,42 @@ def small_configs(torch, yskn_smp, synth, only=0, steps=30, warmup=5):
             r.update(extra)
         res[name] = r
 
+    L = yskn_smp.load_library()
+    sptr = C.c_void_p(stream.cuda_stream)
+
+    def prepared(name, *args):
+        """One C call with arguments built once (device-resident inputs and
+        outputs), so that the timed loop measures the launches only."""
+        f = getattr(L, name)
+
+        def call(i):
+            st = f(*args)
+            if st != 0:
+                raise RuntimeError(L.yskn_smp_last_error().decode())
+        return call
+
+    def vp(t):
+        return C.c_void_p(t.data_ptr())
+
     # 1: single row, 1,024 draws in one launch (and one draw)
     if only in (0, 1):
         x = synth.single_row(dev)
         d = yskn_smp.DeviceSampler(1, synth.V_SMALL)
         d.set_params(yskn_smp.SamplingParameters(temperature_milli=1000, top_p_milli=950, top_k=20, seed=0))
         pos = torch.arange(1024, dtype=torch.int64, device=dev).reshape(1, 1024)
-        o = d.sample(x, pos, argmax=True, top20=True)
-        d.sync()
-        record("single_row_1024_draws", lambda i: d.sample(x, pos, top20=True), synth.V_SMALL * 4,
-               "1 x 151,936 f32, top-k 20, top-p 0.95, T 1.0, 1,024 positions in one call")
+        ids = torch.empty((1, 1024), dtype=torch.int32, device=dev)
+        keep1 = {}
+        aux1 = d._aux(1, dev, keep1, top20=True)
+        record("single_row_1024_draws",
+               prepared("yskn_smp_sample", d.h, vp(x), d._dtype(x), 1, synth.V_SMALL, synth.V_SMALL, vp(pos), 1024,
+                        vp(ids), C.byref(aux1), sptr),
+               synth.V_SMALL * 4, "1 x 151,936 f32, top-k 20, top-p 0.95, T 1.0, 1,024 positions in one call")
         p1 = torch.zeros((1, 1), dtype=torch.int64, device=dev)
-        record("single_row_one_draw", lambda i: d.sample(x, p1), synth.V_SMALL * 4,
-               "1 x 151,936 f32, top-k 20, top-p 0.95, T 1.0, one draw")
+        aux0 = yskn_smp.CAux()
+        record("single_row_one_draw",
+               prepared("yskn_smp_sample", d.h, vp(x), d._dtype(x), 1, synth.V_SMALL, synth.V_SMALL, vp(p1), 1,
+                        vp(ids), C.byref(aux0), sptr),
+               synth.V_SMALL * 4, "1 x 151,936 f32, top-k 20, top-p 0.95, T 1.0, one draw")
     # 2: speculative verify, 8 rows
     if only in (0, 2):
         tgt, _ = synth.spec_verify(8, dev)
@@ -171,8 +194,14 @@ def small_configs(torch, yskn_smp, synth, only=0, steps=30, warmup=5):
         d2.set_params(yskn_smp.SamplingParameters(temperature_milli=1000, top_p_milli=950, top_k=20, seed=0x5EC))
         drafts = torch.zeros(7, dtype=torch.int32, device=dev)
         base = torch.tensor([10_000], dtype=torch.int64, device=dev)
-        record("spec_verify_8", lambda i: d2.verify(tgt, drafts, base), 8 * synth.V_LARGE * 4,
-               "verify 8 x 248,320 f32, top-k 20, top-p 0.95, accept rule on the device")
+        eos = torch.zeros(1, dtype=torch.int32, device=dev)
+        vids = torch.empty(8, dtype=torch.int32, device=dev)
+        vres = torch.empty(5, dtype=torch.int32, device=dev)
+        aux2 = yskn_smp.CAux()
+        record("spec_verify_8",
+               prepared("yskn_smp_verify", d2.h, vp(tgt), d2._dtype(tgt), 8, synth.V_LARGE, synth.V_LARGE,
+                        vp(drafts), vp(base), vp(eos), 0, vp(vids), vp(vres), C.byref(aux2), None, sptr),
+               8 * synth.V_LARGE * 4, "verify 8 x 248,320 f32, top-k 20, top-p 0.95, accept rule on the device")
     # 3: penalties, bf16
     if only in (0, 3):
         xb, hist = synth.penalties(dev)
@@ -180,9 +209,13 @@ def small_configs(torch, yskn_smp, synth, only=0, steps=30, warmup=5):
         d3.set_params(yskn_smp.SamplingParameters(temperature_milli=700, top_p_milli=900, min_p_milli=50,
                                                   top_k=20, seed=31, repetition_penalty=1.05,
                                                   presence_penalty=0.5, frequency_penalty=0.3))
-        h2 = hist.reshape(1, -1)
         p3 = torch.zeros(1, dtype=torch.int64, device=dev)
-        record("penalties_bf16", lambda i: d3.sample(xb, p3, history=h2),
+        ids3 = torch.empty(1, dtype=torch.int32, device=dev)
+        keep3 = {}
+        aux3 = d3._aux(1, dev, keep3, history=hist.reshape(1, -1))
+        record("penalties_bf16",
+               prepared("yskn_smp_sample", d3.h, vp(xb), d3._dtype(xb), 1, synth.V_LARGE, synth.V_LARGE, vp(p3), 1,
+                        vp(ids3), C.byref(aux3), sptr),
                synth.V_LARGE * 2 + hist.numel() * 4,
                "1 x 248,320 bf16 + 8,192 history ids, rep 1.05 pres 0.5 freq 0.3, T 0.7 top-p 0.9 min-p 0.05",
                {"kernels_per_call": 2})
@@ -195,7 +228,12 @@ def small_configs(torch, yskn_smp, synth, only=0, steps=30, warmup=5):
                                                    top_p_milli=p["top_p_milli"], min_p_milli=p["min_p_milli"],
                                                    top_k=p["top_k"], seed=p["seed"]) for p in pr])
         p4 = torch.tensor([p["position"] for p in pr], dtype=torch.int64, device=dev)
-        record("batched_heterogeneous_64", lambda i: d4.sample(xs, p4), 64 * synth.V_LARGE * 4,
+        ids4 = torch.empty(64, dtype=torch.int32, device=dev)
+        aux4 = yskn_smp.CAux()
+        record("batched_heterogeneous_64",
+               prepared("yskn_smp_sample", d4.h, vp(xs), d4._dtype(xs), 64, synth.V_LARGE, synth.V_LARGE, vp(p4), 1,
+                        vp(ids4), C.byref(aux4), sptr),
+               64 * synth.V_LARGE * 4,
                "64 x 248,320 f32, per-row T / top-p / min-p, top-k cycling 1, 20, 50, disabled",
                {"path_stats_after": None})
         res["batched_heterogeneous_64"]["path_stats_after"] = d4.stats()

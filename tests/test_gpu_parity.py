@@ -245,6 +245,43 @@ def test_penalties_small(small_dev):
         assert np.array_equal(out["top20_vals"][r].cpu().numpy().view(np.uint32), y[tt].view(np.uint32))
 
 
+def test_penalties_across_vocabulary_windows():
+    # the history's membership words are built 262,144 ids at a time: ids on
+    # both sides of each window edge, the first and last id, one id repeated
+    # thousands of times and a full 16,384-token history
+    rng = np.random.default_rng(21)
+    V, rows = 700_001, 3
+    x = (2 * rng.standard_normal((rows, V))).astype(np.float32)
+    edges = np.array([0, 31, 32, 262_143, 262_144, 262_145, 524_287, 524_288, V - 1], np.int64)
+    hist = np.empty((rows, 16_384), np.int32)
+    for r in range(rows):
+        h = np.concatenate([np.repeat(edges, np.arange(1, len(edges) + 1) * (r + 1)),
+                            np.full(5000, 400_000 + r),
+                            rng.zipf(1.2, 16_384) % (V - 1000) + 1000])[:16_384]
+        hist[r] = rng.permutation(h)
+        x[r, edges] = 30.0 + rng.random(len(edges)).astype(np.float32)   # all in the top 20
+    hl = np.array([16_384, 9_000, 16_384], np.int32)
+    hist[2, 77] = V                                                      # invalid id
+    sp = SamplingParameters(temperature_milli=900, top_p_milli=950, top_k=20, seed=3,
+                            repetition_penalty=1.05, presence_penalty=0.5, frequency_penalty=0.3)
+    d = DeviceSampler(rows, V, extended_top_k=True)
+    d.set_params(sp)
+    out = d.sample(torch.from_numpy(x).to(DEV), torch.tensor([[9], [10], [11]], device=DEV), top20=True,
+                   row_status=True, history=torch.from_numpy(hist).to(DEV),
+                   history_len=torch.from_numpy(hl).to(DEV))
+    with pytest.raises(InvalidInput):
+        d.sync()
+    assert out["status"].cpu().tolist() == [0, 0, -1]
+    for r in range(2):
+        y = O.apply_penalties(x[r], hist[r, :hl[r]], 1.05, 0.5, 0.3)
+        assert to_u32(out["ids"])[r, 0] == oracle_select(y, 9 + r, sp)
+        tt = O.top_tokens(y, 20)
+        assert set(edges) <= set(tt)
+        assert list(to_u32(out["top20_ids"])[r]) == list(tt)
+        assert np.array_equal(out["top20_vals"][r].cpu().numpy().view(np.uint32), y[tt].view(np.uint32))
+    d.close()
+
+
 def test_top_tokens_and_nll_apis(small_dev):
     rng = np.random.default_rng(13)
     x = (3 * rng.standard_normal((7, 12_345))).astype(np.float32)

@@ -49,9 +49,8 @@ struct yskn_smp {
   uint64_t* d_dense_b = nullptr;
   double* d_dense_w = nullptr;
   int64_t dense_ld = 0;
-  uint32_t* d_pen_bitmap = nullptr;
-  int64_t bm_ld = 0;
-  uint32_t* d_pen_ids = nullptr;
+  uint2* d_pen_words = nullptr;
+  int64_t pw_ld = 0;
   uint32_t* d_pen_cnt = nullptr;
   int32_t* d_pen_len = nullptr;
   unsigned long long* d_stats = nullptr;
@@ -258,9 +257,8 @@ SmpArgs base_args(yskn_smp_handle h, const void* logits, int32_t rows, int32_t v
   a.prm_shared = h->params_shared ? 1 : 0;
   a.n_draws = 1;
   a.status = h->d_status;
-  a.pen_bitmap = h->d_pen_bitmap;
-  a.bm_ld = h->bm_ld;
-  a.pen_ids = h->d_pen_ids;
+  a.pen_words = h->d_pen_words;
+  a.pw_ld = h->pw_ld;
   a.pen_cnt = h->d_pen_cnt;
   a.pen_len = h->d_pen_len;
   a.dense_a = h->d_dense_a;
@@ -293,9 +291,8 @@ int launch(yskn_smp_handle h, SmpArgs& a, int32_t dtype, bool pen, const yskn_sm
     p.history_ld = aux ? aux->history_ld : 0;
     p.V = a.V;
     p.rows = a.rows;
-    p.bitmap = h->d_pen_bitmap;
-    p.bm_ld = h->bm_ld;
-    p.ids = h->d_pen_ids;
+    p.words = h->d_pen_words;
+    p.pw_ld = h->pw_ld;
     p.cnt = h->d_pen_cnt;
     p.len = h->d_pen_len;
     p.prm = h->d_params;
@@ -395,7 +392,7 @@ int yskn_smp_create(int32_t max_rows, int32_t max_vocab, uint32_t flags, yskn_sm
   if (hipGetDevice(&h->device) != hipSuccess) h->device = 0;
   const size_t R = (size_t)max_rows;
   h->dense_ld = ((int64_t)max_vocab + 63) / 64 * 64;
-  h->bm_ld = ((int64_t)max_vocab + 31) / 32;
+  h->pw_ld = ((int64_t)max_vocab + 31) / 32;
   hipError_t e = hipSuccess;
   auto step = [&](hipError_t r) {
     if (e == hipSuccess) e = r;
@@ -407,8 +404,7 @@ int yskn_smp_create(int32_t max_rows, int32_t max_vocab, uint32_t flags, yskn_sm
   step(alloc(&h->d_dense_a, R * (size_t)h->dense_ld));
   step(alloc(&h->d_dense_b, R * (size_t)h->dense_ld));
   step(alloc(&h->d_dense_w, R * (size_t)h->dense_ld));
-  step(alloc(&h->d_pen_bitmap, R * (size_t)h->bm_ld));
-  step(alloc(&h->d_pen_ids, R * (size_t)HCAP));
+  step(alloc(&h->d_pen_words, R * (size_t)h->pw_ld));
   step(alloc(&h->d_pen_cnt, R * (size_t)HCAP));
   step(alloc(&h->d_pen_len, R));
   step(alloc(&h->d_stats, (size_t)STAT_COUNT));
@@ -438,7 +434,7 @@ void yskn_smp_destroy(yskn_smp_handle h) {
   if (!h) return;
   void* ptrs[] = {h->d_params,
                   h->d_status,     h->d_vcount,    h->d_vresult,     h->d_dense_a,
-                  h->d_dense_b,    h->d_dense_w,   h->d_pen_bitmap,  h->d_pen_ids,
+                  h->d_dense_b,    h->d_dense_w,   h->d_pen_words,
                   h->d_pen_cnt,    h->d_pen_len,   h->d_stats,       h->d_host_logits,
                   h->d_host_pos,   h->d_host_out,  h->d_exp_cand,    h->d_exp_meta,
                   h->d_segcnt};

@@ -142,11 +142,10 @@ struct SmpArgs {
   int32_t* status;       // handle's [rows]
   int32_t* row_status;   // caller's [rows] or NULL
   // penalties
-  const uint32_t* pen_bitmap;  // [rows][bm_ld]
-  int64_t bm_ld;
-  const uint32_t* pen_ids;     // [rows][HCAP] sorted unique ids
-  const uint32_t* pen_cnt;     // [rows][HCAP]
-  const int32_t* pen_len;      // [rows], -1 = invalid history
+  const uint2* pen_words;      // [rows][pw_ld] {membership bits, distinct ids below}
+  int64_t pw_ld;
+  const uint32_t* pen_cnt;     // [rows][HCAP] count of each distinct id, in id order
+  const int32_t* pen_len;      // [rows] distinct ids, -1 = invalid history
   // workspace
   uint64_t* dense_a;    // [rows][dense_ld]
   uint64_t* dense_b;
@@ -169,9 +168,8 @@ struct PenArgs {
   int64_t history_ld;
   int32_t V;
   int32_t rows;
-  uint32_t* bitmap;
-  int64_t bm_ld;
-  uint32_t* ids;
+  uint2* words;
+  int64_t pw_ld;
   uint32_t* cnt;
   int32_t* len;
   const DevParams* prm;

@@ -17,8 +17,8 @@
 //             (output_head_sampler.rs:136-212). Rows with more candidates
 //             than LDS holds take the exact "dense" path: radix select, stable
 //             LSD radix sort in global scratch, same tail.
-//  smp_penalty_prep (penalties only) sorts each row's history into unique
-//             ids, counts and a membership bitmap.
+//  smp_penalty_prep (penalties only) turns each row's history into
+//             membership words over the vocabulary and per-id counts.
 //
 // Ordering is (value desc, id asc) everywhere, as output_head_sampler.rs:
 // 124-132; -0 and +0 compare equal (keys canonicalise -0 to +0) and ties go
@@ -319,20 +319,17 @@ struct RowCtx {
   float us, r;             // common scale, inverse RMS of the row
   const float* lout;       // the row's logits written out (re-reads), or NULL
   float* loutw;            // the same, to write (or NULL)
-  const uint32_t* bitmap;  // penalty bitmap of the row (or NULL)
-  const uint32_t* pids;
+  // Penalty words of the row (or NULL): word w holds the history membership
+  // bits of ids 32w..32w+31 and the number of distinct history ids below 32w,
+  // the index into pcnt of the word's first member.
+  const uint2* pw;
   const uint32_t* pcnt;
-  int32_t plen;
   float rep, pres, freq;
 };
 
-__device__ __forceinline__ uint32_t pen_count(const RowCtx& r, uint32_t v) {
-  int lo = 0, hi = r.plen;
-  while (lo < hi) {
-    const int mid = (lo + hi) >> 1;
-    if (r.pids[mid] < v) lo = mid + 1; else hi = mid;
-  }
-  return (lo < r.plen && r.pids[lo] == v) ? r.pcnt[lo] : 0u;
+// History count of a member id whose penalty word is w.
+__device__ __forceinline__ uint32_t pen_count(const RowCtx& r, uint2 w, uint32_t v) {
+  return r.pcnt[w.y + __popc(w.x & ((1u << (v & 31)) - 1u))];
 }
 
 // Penalties in binary32 round-to-nearest, each operation separately rounded.
@@ -368,8 +365,9 @@ __device__ __forceinline__ uint32_t raw_bits(const RowCtx& r, int64_t i) {
 template <int DT, bool PEN>
 __device__ __forceinline__ uint32_t value_bits(const RowCtx& r, int64_t i) {
   uint32_t b = raw_bits<DT>(r, i);
-  if (PEN && r.bitmap) {
-    if ((r.bitmap[i >> 5] >> (i & 31)) & 1u) b = penalize(b, pen_count(r, (uint32_t)i), r);
+  if (PEN && r.pw) {
+    const uint2 w = r.pw[i >> 5];
+    if ((w.x >> (i & 31)) & 1u) b = penalize(b, pen_count(r, w, (uint32_t)i), r);
   }
   return b;
 }
@@ -1154,21 +1152,16 @@ __device__ __forceinline__ RowCtx make_rowctx(const SmpArgs& A, const DevParams&
       rc.lout = rc.loutw;
     }
   }
-  rc.bitmap = nullptr;
-  rc.pids = nullptr;
+  rc.pw = nullptr;
   rc.pcnt = nullptr;
-  rc.plen = 0;
   rc.rep = P.rep;
   rc.pres = P.pres;
   rc.freq = P.freq;
   if (PEN && P.penalize) {
-    rc.plen = A.pen_len[row];
-    if (rc.plen < 0) {
+    if (A.pen_len[row] < 0) {
       *flags |= F_INVALID;
-      rc.plen = 0;
     } else {
-      rc.bitmap = A.pen_bitmap + (int64_t)row * A.bm_ld;
-      rc.pids = A.pen_ids + (int64_t)row * HCAP;
+      rc.pw = A.pen_words + (int64_t)row * A.pw_ld;
       rc.pcnt = A.pen_cnt + (int64_t)row * HCAP;
     }
   }
@@ -1313,61 +1306,62 @@ __device__ void sort_desc_small(uint64_t* a, uint64_t* b, int n) {
   __syncthreads();
 }
 
-// The k-th largest key (1 <= k <= n) among n packed entries in LDS: four
-// 8-bit radix passes from the top; wave 0 finds each pass's digit from
-// suffix sums over the 256-bin histogram (four bins per lane). hist: 256
-// LDS words, bc: 2 more. Block-wide; every thread returns the key.
-__device__ uint32_t lds_kth_key(const uint64_t* buf, uint32_t n, uint32_t k, uint32_t* hist, uint32_t* bc) {
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+// The exact k-th largest key among n >= k packed entries in LDS: four 8-bit
+// radix passes from the top. Each wave adds its lanes' digits with one LDS
+// atomic per distinct digit (ballot-matched peers), and every wave picks the
+// next digit from the histogram itself, so a pass costs one barrier; the
+// three histograms rotate (hist: 768 LDS words), the one of pass p - 1
+// cleared after pass p's barrier. Block-wide; every thread returns the key.
+__device__ uint32_t lds_kth_key(const uint64_t* buf, uint32_t n, uint32_t k, uint32_t* hist) {
+  const int tid = threadIdx.x, lane = tid & 63;
+  for (int i = tid; i < 3 * 256; i += NT) hist[i] = 0u;
+  __syncthreads();
   uint32_t prefix = 0u, mask = 0u, need = k;
   for (int pass = 0; pass < 4; ++pass) {
     const int shift = 24 - 8 * pass;
-    for (int i = tid; i < 256; i += NT) hist[i] = 0u;
-    __syncthreads();
-    for (uint32_t i = (uint32_t)tid; i < n; i += NT) {
-      const uint32_t kk = pk_key(buf[i]);
-      if ((kk & mask) == prefix) atomicAdd(&hist[(kk >> shift) & 255u], 1u);
+    uint32_t* const h = hist + (pass % 3) * 256;
+    for (uint32_t i0 = 0; i0 < n; i0 += NT) {
+      const uint32_t i = i0 + (uint32_t)tid;
+      const uint32_t kk = i < n ? pk_key(buf[i]) : 0u;
+      hist_add8(h, (kk >> shift) & 255u, i < n && (kk & mask) == prefix);
     }
     __syncthreads();
-    if (wave == 0) {
-      uint32_t h[4], own = 0u;
+    // (the histogram of pass 0 serves again in pass 3)
+    if (pass == 1)
+      for (int i = tid; i < 256; i += NT) hist[i] = 0u;
+    uint32_t hq[4], own = 0u;
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        h[q] = hist[4 * lane + q];
-        own += h[q];
-      }
-      // suffix sum: entries in the bins of this lane and every higher lane
-      uint32_t suf = own;
+    for (int q = 0; q < 4; ++q) {
+      hq[q] = h[4 * lane + q];
+      own += hq[q];
+    }
+    // suffix sum: entries in the bins of this lane and every higher lane
+    uint32_t suf = own;
 #pragma unroll
-      for (int o = 1; o < 64; o <<= 1) {
-        const uint32_t t = __shfl_down(suf, o);
-        if (lane + o < 64) suf += t;
-      }
-      const uint64_t reach = __ballot(suf >= need);
-      const int L = reach ? 63 - __builtin_clzll(reach) : -1;  // the highest lane still holding the k-th
-      if (L < 0 && lane == 0) {
-        bc[0] = 0u;  // fewer than k entries (the caller does not ask for that)
-        bc[1] = 1u;
-      }
-      if (lane == L) {
-        uint32_t cum = suf - own;                 // entries in higher lanes' bins
-        int dsel = 4 * L;
-        for (int q = 3; q >= 0; --q) {
-          if (cum + h[q] >= need) {
-            dsel = 4 * L + q;
-            break;
-          }
-          cum += h[q];
+    for (int o = 1; o < 64; o <<= 1) {
+      const uint32_t t = __shfl_down(suf, o);
+      if (lane + o < 64) suf += t;
+    }
+    const uint64_t reach = __ballot(suf >= need);
+    uint32_t dsel = 0u, nn = 1u;  // (fewer than k entries: the caller does not ask for that)
+    if (reach) {
+      const int L = 63 - __builtin_clzll(reach);  // the highest lane still holding the k-th
+      uint32_t cum = suf - own;                     // entries in higher lanes' bins
+      uint32_t d = 4u * (uint32_t)lane;
+#pragma unroll
+      for (int q = 3; q >= 0; --q) {
+        if (cum + hq[q] >= need) {
+          d = 4u * (uint32_t)lane + (uint32_t)q;
+          break;
         }
-        bc[0] = (uint32_t)dsel;
-        bc[1] = need - cum;
+        cum += hq[q];
       }
+      dsel = (uint32_t)__builtin_amdgcn_readlane((int)d, L);
+      nn = (uint32_t)__builtin_amdgcn_readlane((int)(need - cum), L);
     }
-    __syncthreads();
-    prefix |= bc[0] << shift;
+    prefix |= dsel << shift;
     mask |= 255u << shift;
-    need = bc[1];
-    __syncthreads();
+    need = nn;
   }
   return prefix;
 }
@@ -1522,17 +1516,16 @@ __device__ __forceinline__ void chunk_values(const RowCtx& rc, int32_t V, int c,
   const int32_t lim = V - (int32_t)eb;
 #pragma unroll
   for (int q = 0; q < NGRP; ++q) {
-    uint32_t wbits = 0;
-    if (PEN && rc.bitmap && q * 64 * GRP < lim) wbits = rc.bitmap[(eb + q * 64 * GRP) >> 5];
+    uint2 pw = make_uint2(0u, 0u);
+    if (PEN && rc.pw && q * 64 * GRP < lim) pw = rc.pw[(eb + q * 64 * GRP) >> 5];
 #pragma unroll
     for (int j = 0; j < GRP; ++j) {
       const int32_t o = q * 64 * GRP + j;
       uint32_t b = kb[q * GRP + j];
       float v = -__builtin_inff();
       if (full || o < lim) {
-        if (PEN && rc.bitmap && ((wbits >> ((eb + o) & 31)) & 1u)) {
-          const uint32_t e = eb + (uint32_t)o;
-          b = penalize(b, pen_count(rc, e), rc);
+        if (PEN && rc.pw && ((pw.x >> ((eb + o) & 31)) & 1u)) {
+          b = penalize(b, pen_count(rc, pw, eb + (uint32_t)o), rc);
         }
         v = __uint_as_float(b);
         bad |= __builtin_amdgcn_class(v, 0x207) != 0;  // signaling/quiet NaN, +-inf
@@ -1935,17 +1928,40 @@ __global__ __launch_bounds__(NT) void smp_row(SmpArgs A) {
       if (first || __ballot(lk > lb || lk > ws.wkey)) {
         uint32_t rk = lk;
         const int rr = first ? r_first : r_next;
-        for (int i = 0; i < rr; ++i) {
-          const uint32_t m = wave_max_dpp(rk);
-          if (i == 0) cmax = m;
-          if (m <= theta_w || m <= th_row) break;  // 0, cannot enter the full list, or below the row bound
-          // insert m: entries >= m keep their lanes, the rest move up by one
-          const uint32_t pos = (uint32_t)__popcll(__ballot(lane < plan.KB && lst >= m));
-          const uint32_t up = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)lst, 0x138, 0xf, 0xf, false);  // wave_shr:1
-          lst = (uint32_t)lane < pos ? lst : ((uint32_t)lane == pos ? m : up);
+        if (first && rr > 2) {
+          // The wave's first chunk with the list empty (th_row = theta_w =
+          // 0): the list becomes the rr largest nonzero lane maxima, equal
+          // values once per lane, in one step -- the rr-th largest by a
+          // ballot radix select, each qualifying lane's rank by (value desc,
+          // lane asc) over the qualifying lanes, and one lane permute.
+          cmax = wave_max_dpp(lk);
+          const int nz = __popcll(__ballot(lk != 0u));
+          const uint32_t kth = nz > rr ? wave_kth_largest_radix(lk, rr) : 1u;
+          const uint64_t in = __ballot(lk != 0u && lk >= kth);
+          uint32_t rank = 0u;
+          for (uint64_t rem = in; rem; rem &= rem - 1ull) {
+            const int b = __builtin_ctzll(rem);
+            const uint32_t vb = (uint32_t)__builtin_amdgcn_readlane((int)lk, b);
+            rank += (vb > lk || (vb == lk && b < lane)) ? 1u : 0u;
+          }
+          const bool put = ((in >> lane) & 1ull) != 0ull && rank < (uint32_t)rr;
+          const uint32_t got = (uint32_t)__builtin_amdgcn_ds_permute((int)((put ? rank : 63u) * 4u), (int)lk);
+          const int nput = __popcll(in) < rr ? __popcll(in) : rr;
+          lst = lane < nput ? got : 0u;
           theta_w = (uint32_t)__builtin_amdgcn_readlane((int)lst, plan.KB - 1);
-          const uint64_t eq = __ballot(rk == m);
-          if (lane == (int)__builtin_ctzll(eq)) rk = 0u;
+        } else {
+          for (int i = 0; i < rr; ++i) {
+            const uint32_t m = wave_max_dpp(rk);
+            if (i == 0) cmax = m;
+            if (m <= theta_w || m <= th_row) break;  // 0, cannot enter the full list, or below the row bound
+            // insert m: entries >= m keep their lanes, the rest move up by one
+            const uint32_t pos = (uint32_t)__popcll(__ballot(lane < plan.KB && lst >= m));
+            const uint32_t up = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)lst, 0x138, 0xf, 0xf, false);  // wave_shr:1
+            lst = (uint32_t)lane < pos ? lst : ((uint32_t)lane == pos ? m : up);
+            theta_w = (uint32_t)__builtin_amdgcn_readlane((int)lst, plan.KB - 1);
+            const uint64_t eq = __ballot(rk == m);
+            if (lane == (int)__builtin_ctzll(eq)) rk = 0u;
+          }
         }
         if (cmax > ws.wkey) {
           ws.wkey = cmax;
@@ -2255,14 +2271,29 @@ __global__ __launch_bounds__(NT) void smp_row(SmpArgs A) {
     __syncthreads();
     const uint32_t total = sh.count;
     if (total <= (uint32_t)BUFCAP) {
+      // every load of the thread is issued before the first is waited for
+      // (one round trip, not one per slot)
       const uint64_t* const xr = A.exp_cand + (int64_t)row * nseg * EXP_CAP;
-      for (int i = tid; i < nseg * EXP_CAP; i += NT) {
+      constexpr int IMP = SEG_MAX * EXP_CAP / NT;
+      uint64_t v[IMP];
+      uint32_t dst[IMP];
+#pragma unroll
+      for (int r = 0; r < IMP; ++r) {
+        const int i = tid + r * NT;
         const int q = i / EXP_CAP, j = i - q * EXP_CAP;
-        if ((uint32_t)j < s_off[SEG_MAX + q]) fl.buf[s_off[q] + (uint32_t)j] = xr[i];
+        dst[r] = 0xffffffffu;
+        v[r] = 0ull;
+        if (q < nseg && (uint32_t)j < s_off[SEG_MAX + q]) {
+          dst[r] = s_off[q] + (uint32_t)j;
+          v[r] = xr[i];
+        }
       }
+#pragma unroll
+      for (int r = 0; r < IMP; ++r)
+        if (dst[r] != 0xffffffffu) fl.buf[dst[r]] = v[r];
       __syncthreads();
       theta = total >= (uint32_t)plan.KB
-                  ? lds_kth_key(fl.buf, total, (uint32_t)plan.KB, (uint32_t*)fl.cand, (uint32_t*)fl.cand + 256)
+                  ? lds_kth_key(fl.buf, total, (uint32_t)plan.KB, (uint32_t*)fl.cand)
                   : 0u;
     } else {
       theta = 0u;
@@ -2571,94 +2602,115 @@ __global__ __launch_bounds__(NT) void smp_row(SmpArgs A) {
   }
 }
 // ---------------------------------------------------------------------------
-// Penalty preparation: per row, sorted unique history ids with counts and a
-// membership bitmap over the vocabulary.
+// Penalty preparation: the number of times each token occurs in the row's
+// history (the frequency penalty's count; presence and repetition apply to
+// any count > 0), laid out for a one-load lookup. Per row, word w of the vocabulary holds the membership bits of ids
+// 32w..32w+31 and the number of distinct history ids below 32w; the counts of
+// the distinct ids follow in id order, so id v's count is
+// cnt[rank(w) + popcount(bits(w) below v)]. Built in LDS, a window of PW_WIN
+// words at a time, with no sort: the history sits in registers (HCAP / 1024
+// ids per thread), membership by LDS atomicOr, ranks by a block scan of the
+// words' popcounts, counts by LDS atomicAdd at each id's rank.
 // ---------------------------------------------------------------------------
-__global__ __launch_bounds__(1024) void smp_penalty_prep(PenArgs A) {
-  __shared__ uint32_t h[HCAP];
-  __shared__ int red[16];
+constexpr int PP_NT = 1024;
+constexpr int PP_PER = HCAP / PP_NT;
+constexpr int PW_WIN = 8192;
+constexpr int PW_PT = PW_WIN / PP_NT;
+static_assert(PP_PER * PP_NT == HCAP && PW_PT * PP_NT == PW_WIN, "penalty prep geometry");
+
+__global__ __launch_bounds__(PP_NT) void smp_penalty_prep(PenArgs A) {
+  __shared__ uint32_t wb[PW_WIN];  // the window's membership bits
+  __shared__ uint32_t wr[PW_WIN];  // the window's ranks
+  __shared__ uint32_t cnt[HCAP];
+  __shared__ uint32_t red[PP_NT / 64];
   __shared__ int s_bad;
-  const int tid = threadIdx.x, row = blockIdx.x;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, row = blockIdx.x;
   const DevParams P = A.prm[A.prm_shared ? 0 : row];
   if (!P.penalize) {
     if (tid == 0) A.len[row] = 0;
     return;
   }
-  int len = A.history_len ? A.history_len[row] : 0;
-  uint32_t* bm = A.bitmap + (int64_t)row * A.bm_ld;
-  const int words = (A.V + 31) >> 5;
-  for (int i = tid; i < words; i += 1024) bm[i] = 0u;
-  if (tid == 0) s_bad = (len < 0 || len > HCAP || (A.history_ld > 0 && (int64_t)len > A.history_ld)) ? 1 : 0;
-  __syncthreads();
-  if (s_bad) {
+  const int len = A.history_len ? A.history_len[row] : 0;
+  if (len < 0 || len > HCAP || (A.history_ld > 0 && (int64_t)len > A.history_ld)) {
     if (tid == 0) A.len[row] = -1;
     return;
   }
-  int n2 = 1;
-  while (n2 < len) n2 <<= 1;
-  for (int i = tid; i < n2; i += 1024) {
-    uint32_t v = 0xffffffffu;
+  // ids >= V are invalid; 0xffffffff (>= any V) marks an empty slot
+  uint32_t h[PP_PER];
+  bool bad = false;
+#pragma unroll
+  for (int k = 0; k < PP_PER; ++k) {
+    const int i = tid + k * PP_NT;
+    h[k] = 0xffffffffu;
     if (i < len) {
-      v = A.history[(int64_t)row * A.history_ld + i];
-      if (v >= (uint32_t)A.V) atomicOr(&s_bad, 1);
+      h[k] = A.history[(int64_t)row * A.history_ld + i];
+      bad |= h[k] >= (uint32_t)A.V;
     }
-    h[i] = v;
   }
+  if (tid == 0) s_bad = 0;
+  for (int i = tid; i < HCAP; i += PP_NT) cnt[i] = 0u;
+  __syncthreads();
+  if (bad) atomicOr(&s_bad, 1);
   __syncthreads();
   if (s_bad) {
     if (tid == 0) A.len[row] = -1;
     return;
   }
-  // bitonic sort ascending
-  for (int k = 2; k <= n2; k <<= 1) {
-    for (int j = k >> 1; j > 0; j >>= 1) {
-      for (int i = tid; i < n2; i += 1024) {
-        const int ixj = i ^ j;
-        if (ixj > i) {
-          const uint32_t a = h[i], b = h[ixj];
-          const bool asc = (i & k) == 0;
-          if (asc ? (a > b) : (a < b)) {
-            h[i] = b;
-            h[ixj] = a;
-          }
-        }
+  const int words = (A.V + 31) >> 5;
+  uint2* out = A.words + (int64_t)row * A.pw_ld;
+  uint32_t carry = 0;  // distinct ids below the window
+  for (int w0 = 0; w0 < words; w0 += PW_WIN) {
+    const int nw = min(PW_WIN, words - w0);
+#pragma unroll
+    for (int j = 0; j < PW_PT; ++j) wb[tid * PW_PT + j] = 0u;
+    __syncthreads();
+#pragma unroll
+    for (int k = 0; k < PP_PER; ++k) {
+      const int w = (int)(h[k] >> 5) - w0;
+      if (h[k] != 0xffffffffu && w >= 0 && w < nw) atomicOr(&wb[w], 1u << (h[k] & 31));
+    }
+    __syncthreads();
+    uint32_t s = 0;
+#pragma unroll
+    for (int j = 0; j < PW_PT; ++j) s += __popc(wb[tid * PW_PT + j]);
+    uint32_t inc = s;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const uint32_t y = __shfl_up(inc, o);
+      if (lane >= o) inc += y;
+    }
+    if (lane == 63) red[wave] = inc;
+    __syncthreads();
+    uint32_t r = carry, tot = 0;
+#pragma unroll
+    for (int w = 0; w < PP_NT / 64; ++w) {
+      r += (w < wave) ? red[w] : 0u;
+      tot += red[w];
+    }
+    r += inc - s;
+#pragma unroll
+    for (int j = 0; j < PW_PT; ++j) {
+      const int wi = tid * PW_PT + j;
+      wr[wi] = r;
+      r += __popc(wb[wi]);
+    }
+    __syncthreads();
+    // coalesced: consecutive threads write consecutive words
+    for (int wi = tid; wi < nw; wi += PP_NT) out[w0 + wi] = make_uint2(wb[wi], wr[wi]);
+#pragma unroll
+    for (int k = 0; k < PP_PER; ++k) {
+      const int w = (int)(h[k] >> 5) - w0;
+      if (h[k] != 0xffffffffu && w >= 0 && w < nw) {
+        const uint32_t below = wb[w] & ((1u << (h[k] & 31)) - 1u);
+        atomicAdd(&cnt[wr[w] + __popc(below)], 1u);
       }
-      __syncthreads();
     }
+    carry += tot;
+    __syncthreads();
   }
-  // run starts: count per thread over a contiguous chunk, then scan
-  const int chunk = (len + 1023) / 1024;
-  const int lo = tid * chunk, hi = min(len, lo + chunk);
-  int starts = 0;
-  for (int i = lo; i < hi; ++i) starts += (i == 0 || h[i] != h[i - 1]) ? 1 : 0;
-  // block exclusive scan (1024 threads = 16 waves)
-  const int lane = tid & 63, wave = tid >> 6;
-  int inc = starts;
-  for (int o = 1; o < 64; o <<= 1) {
-    const int y = __shfl_up(inc, o);
-    if (lane >= o) inc += y;
-  }
-  if (lane == 63) red[wave] = inc;
-  __syncthreads();
-  int base = 0, tot = 0;
-  for (int w = 0; w < 16; ++w) {
-    base += (w < wave) ? red[w] : 0;
-    tot += red[w];
-  }
-  int u = base + inc - starts;
-  uint32_t* ids = A.ids + (int64_t)row * HCAP;
-  uint32_t* cnt = A.cnt + (int64_t)row * HCAP;
-  for (int i = lo; i < hi; ++i) {
-    if (i == 0 || h[i] != h[i - 1]) {
-      int e = i + 1;
-      while (e < len && h[e] == h[i]) ++e;
-      ids[u] = h[i];
-      cnt[u] = (uint32_t)(e - i);
-      atomicOr(&bm[h[i] >> 5], 1u << (h[i] & 31));
-      ++u;
-    }
-  }
-  if (tid == 0) A.len[row] = tot;
+  uint32_t* co = A.cnt + (int64_t)row * HCAP;
+  for (int i = tid; i < (int)carry; i += PP_NT) co[i] = cnt[i];
+  if (tid == 0) A.len[row] = (int32_t)carry;
 }
 
 // ---------------------------------------------------------------------------
