@@ -8,7 +8,11 @@
 // 16-byte-per-lane device copy of the same byte count instead, whose counters
 // calibrate the sampler's.
 //
-//   smp_bench [--logits FILE] [--rows R] [--vocab V] [--steps K] [--warmup W] [--copy]
+//   smp_bench [--logits FILE] [--rows R] [--vocab V] [--steps K] [--warmup W]
+//             [--top-k K] [--logprobs N] [--copy]
+//
+// --top-k sets every row's top-k (default 0, disabled); --logprobs the
+// number of logprobs per row (default 20, 0 for none).
 //
 // FILE holds rows * V little-endian binary32 values (row-major). Without it
 // the logits come from an on-device generator of 2 * t_3 variates (a
@@ -77,7 +81,7 @@ void check(int st, const char* what) {
 
 int main(int argc, char** argv) {
   const char* path = nullptr;
-  int rows = 256, V = 248320, steps = 20, warmup = 3;
+  int rows = 256, V = 248320, steps = 20, warmup = 3, top_k = 0, n_lp = 20;
   bool copy = false;
   for (int i = 1; i < argc; ++i) {
     const bool more = i + 1 < argc;
@@ -86,15 +90,18 @@ int main(int argc, char** argv) {
     else if (!strcmp(argv[i], "--vocab") && more) V = atoi(argv[++i]);
     else if (!strcmp(argv[i], "--steps") && more) steps = atoi(argv[++i]);
     else if (!strcmp(argv[i], "--warmup") && more) warmup = atoi(argv[++i]);
+    else if (!strcmp(argv[i], "--top-k") && more) top_k = atoi(argv[++i]);
+    else if (!strcmp(argv[i], "--logprobs") && more) n_lp = atoi(argv[++i]);
     else if (!strcmp(argv[i], "--copy")) copy = true;
     else {
-      fprintf(stderr, "usage: %s [--logits FILE] [--rows R] [--vocab V] [--steps K] [--warmup W] [--copy]\n",
+      fprintf(stderr, "usage: %s [--logits FILE] [--rows R] [--vocab V] [--steps K] [--warmup W] [--top-k K] "
+                      "[--logprobs N] [--copy]\n",
               argv[0]);
       return 2;
     }
   }
-  if (rows < 1 || V < 1 || steps < 1 || warmup < 0) {
-    fprintf(stderr, "rows, vocab and steps must be positive\n");
+  if (rows < 1 || V < 1 || steps < 1 || warmup < 0 || top_k < 0 || n_lp < 0 || n_lp > 64) {
+    fprintf(stderr, "rows, vocab and steps must be positive, top-k >= 0, logprobs in 0..64\n");
     return 2;
   }
   const size_t n = (size_t)rows * V, bytes = n * sizeof(float);
@@ -155,7 +162,7 @@ int main(int argc, char** argv) {
     prm[r] = yskn_smp_params{};
     prm[r].temperature_milli = 1000;
     prm[r].top_p_milli = 950;
-    prm[r].top_k = 0;
+    prm[r].top_k = (uint32_t)top_k;
     prm[r].min_p_milli = 0;
     prm[r].seed = yskn::mix64(0x1A46Eull + (uint64_t)r);
     prm[r].version = YSKN_SMP_VERSION_GUMBEL;
@@ -171,14 +178,14 @@ int main(int argc, char** argv) {
   int32_t* d_st;
   HIP_OK(hipMalloc(&d_pos, rows * sizeof(uint64_t)));
   HIP_OK(hipMalloc(&d_ids, rows * sizeof(uint32_t)));
-  HIP_OK(hipMalloc(&d_lpi, rows * 20 * sizeof(uint32_t)));
-  HIP_OK(hipMalloc(&d_lp, rows * 20 * sizeof(double)));
+  HIP_OK(hipMalloc(&d_lpi, rows * 64 * sizeof(uint32_t)));
+  HIP_OK(hipMalloc(&d_lp, rows * 64 * sizeof(double)));
   HIP_OK(hipMalloc(&d_st, rows * sizeof(int32_t)));
   HIP_OK(hipMemcpy(d_pos, pos.data(), rows * sizeof(uint64_t), hipMemcpyHostToDevice));
   yskn_smp_aux aux{};
-  aux.n_logprobs = 20;
-  aux.logprob_ids = d_lpi;
-  aux.logprobs = d_lp;
+  aux.n_logprobs = n_lp;
+  aux.logprob_ids = n_lp ? d_lpi : nullptr;
+  aux.logprobs = n_lp ? d_lp : nullptr;
   aux.row_status = d_st;
 
   auto step = [&](int i) {

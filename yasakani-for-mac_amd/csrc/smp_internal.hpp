@@ -66,7 +66,7 @@ struct SegMeta {
   uint32_t count;     // candidates exported (> EXP_CAP: overflow, none kept)
   uint32_t flags;     // F_* seen in the segment
   uint32_t mkey;      // the segment's largest key (0: none finite)
-  uint32_t pad;
+  uint32_t theta;     // the segment's certified KB-th key: no larger than the row's
   double mass;        // sum of exp(l - mref) over the segment's mass terms
   float mref;         // reference point of that mass (-inf: no terms)
   float pad2;

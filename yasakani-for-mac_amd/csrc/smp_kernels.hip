@@ -192,6 +192,20 @@ __device__ __forceinline__ uint32_t wave_kth_largest_radix(uint32_t x, int k) {
   }
   return t;
 }
+// k-th largest (1 <= k <= 256) of up to four values per lane (zeros for
+// absent ones): the same bitwise ballot radix select over 256 values.
+__device__ __forceinline__ uint32_t wave_kth_largest_radix4(const uint32_t (&x)[4], int k) {
+  uint32_t t = 0u;
+#pragma unroll
+  for (int b = 31; b >= 0; --b) {
+    const uint32_t u = t | (1u << b);
+    uint32_t c = 0u;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) c += (uint32_t)__popcll(__ballot(x[q] >= u));
+    if (c >= (uint32_t)k) t = u;
+  }
+  return t;
+}
 __device__ __forceinline__ int wave_sum_int(int v) {
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
@@ -1091,6 +1105,7 @@ __device__ void lsd_sort_desc(uint64_t* a, uint64_t* b, int64_t n, uint32_t* lds
 
 static_assert(BUFCAP >= NT * 8, "the append buffer holds a sort tile");
 static_assert(2 * CAP >= 5888, "the candidate array holds the sort's counters");
+static_assert(2 * CAP >= 2 * SEG_MAX + 2 + 256, "the weights array holds the segment import's tables");
 
 // The dense path's candidates: every element with key >= theta, sorted
 // (value desc, id asc) in dense_a. theta is the smaller of the KB-th
@@ -2213,6 +2228,7 @@ __global__ __launch_bounds__(NT) void smp_row(SmpArgs A) {
         m.count = nx;
         m.flags = sh.flags;
         m.mkey = mk_s;
+        m.theta = theta;
         m.mass = ms;
         m.mref = mr_s;
       }
@@ -2230,16 +2246,31 @@ __global__ __launch_bounds__(NT) void smp_row(SmpArgs A) {
     __syncthreads();
     if (!s_last) return;  // (uniform: the whole block leaves)
     // ---- the row's last block: gather every segment's export ---------------
+    // Every slot of every segment is requested before the segments' records
+    // arrive (their counts then pick the filled slots): one round trip.
+    const uint64_t* const xr = A.exp_cand + (int64_t)row * nseg * EXP_CAP;
+    constexpr int IMP = SEG_MAX * EXP_CAP / NT;
+    uint64_t v[IMP];
+#pragma unroll
+    for (int r = 0; r < IMP; ++r) {
+      const int i = tid + r * NT;
+      v[r] = i < nseg * EXP_CAP ? xr[i] : 0ull;
+    }
     const SegMeta* const mt = A.exp_meta + (int64_t)row * nseg;
-    uint32_t* const s_off = (uint32_t*)fl.w;  // per-segment offsets into the buffer, then its counts
+    // per-segment offsets into the buffer, then its counts; then the largest
+    // segment bound, the number of entries at or above it and their keys
+    // (the first 256)
+    uint32_t* const s_off = (uint32_t*)fl.w;
+    uint32_t* const s_hi = s_off + 2 * SEG_MAX;
     if (wave == 0) {
       // lane q reads segment q's record (one round trip for all of them)
-      uint32_t c = 0u, mk = 0u, fo = 0u;
+      uint32_t c = 0u, mk = 0u, fo = 0u, ts = 0u;
       float mr = -__builtin_inff();
       double ms = 0.0;
       if (lane < nseg) {
         c = mt[lane].count;
         mk = mt[lane].mkey;
+        ts = mt[lane].theta;
         fo = mt[lane].flags;
         mr = mt[lane].mref;
         ms = mt[lane].mass;
@@ -2255,6 +2286,7 @@ __global__ __launch_bounds__(NT) void smp_row(SmpArgs A) {
       }
       const uint32_t total = (uint32_t)__builtin_amdgcn_readlane(incl, 63);
       const uint32_t mkr = wave_max_dpp(mk);
+      const uint32_t tlo = wave_max_dpp(ts);
       uint32_t fr = fo;
 #pragma unroll
       for (int o = 32; o > 0; o >>= 1) fr |= (uint32_t)__shfl_xor((int)fr, o);
@@ -2265,36 +2297,48 @@ __global__ __launch_bounds__(NT) void smp_row(SmpArgs A) {
         // an overflow sends the row to the dense path (a count past the spill)
         sh.count = over ? (uint32_t)BUFCAP + (uint32_t)A.dense_ld + 1u : total;
         sh.ctr = 0u;
+        s_hi[0] = tlo;
+        s_hi[1] = 0u;
       }
     }
     n_mass = nseg;
     __syncthreads();
     const uint32_t total = sh.count;
     if (total <= (uint32_t)BUFCAP) {
-      // every load of the thread is issued before the first is waited for
-      // (one round trip, not one per slot)
-      const uint64_t* const xr = A.exp_cand + (int64_t)row * nseg * EXP_CAP;
-      constexpr int IMP = SEG_MAX * EXP_CAP / NT;
-      uint64_t v[IMP];
-      uint32_t dst[IMP];
+      // The row's KB-th key is among the entries at or above the largest
+      // segment bound (that segment exported at least KB of them, and every
+      // segment exported all of its own): at most 256 of them, one wave
+      // selects it (every wave, the same); more, the whole import is ranked.
+      const uint32_t tlo = s_hi[0];
 #pragma unroll
       for (int r = 0; r < IMP; ++r) {
         const int i = tid + r * NT;
         const int q = i / EXP_CAP, j = i - q * EXP_CAP;
-        dst[r] = 0xffffffffu;
-        v[r] = 0ull;
-        if (q < nseg && (uint32_t)j < s_off[SEG_MAX + q]) {
-          dst[r] = s_off[q] + (uint32_t)j;
-          v[r] = xr[i];
+        const bool ok = q < nseg && (uint32_t)j < s_off[SEG_MAX + q];
+        if (ok) fl.buf[s_off[q] + (uint32_t)j] = v[r];
+        const uint32_t key = pk_key(v[r]);
+        const bool hi = ok && key >= tlo;
+        const uint64_t hm = __ballot(hi);
+        if (hm) {
+          uint32_t base = 0u;
+          if (lane == 0) base = atomicAdd(&s_hi[1], (uint32_t)__popcll(hm));
+          base = (uint32_t)__builtin_amdgcn_readfirstlane((int)base);
+          const uint32_t slot = base + lanes_below(hm);
+          if (hi && slot < 256u) s_hi[2 + slot] = key;
         }
       }
-#pragma unroll
-      for (int r = 0; r < IMP; ++r)
-        if (dst[r] != 0xffffffffu) fl.buf[dst[r]] = v[r];
       __syncthreads();
-      theta = total >= (uint32_t)plan.KB
-                  ? lds_kth_key(fl.buf, total, (uint32_t)plan.KB, (uint32_t*)fl.cand)
-                  : 0u;
+      const uint32_t nhi = s_hi[1];
+      if (total < (uint32_t)plan.KB) {
+        theta = 0u;
+      } else if (nhi >= (uint32_t)plan.KB && nhi <= 256u) {
+        uint32_t x[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) x[q] = (uint32_t)(lane + 64 * q) < nhi ? s_hi[2 + lane + 64 * q] : 0u;
+        theta = wave_kth_largest_radix4(x, plan.KB);
+      } else {
+        theta = lds_kth_key(fl.buf, total, (uint32_t)plan.KB, (uint32_t*)fl.cand);
+      }
     } else {
       theta = 0u;
     }
