@@ -2463,12 +2463,15 @@ __global__ __launch_bounds__(NT) void smp_row(SmpArgs A) {
         zfail = !(z - z == 0.0);
         __syncthreads();
       }
+      // the first 64 sorted candidates in LDS too: every output and the
+      // one-wave tail read only those (LDS reads, not generic ones)
+      for (int i = tid; i < 64; i += NT) fl.cand[i] = i < ncand ? cand[i] : 0ull;
     }
 
     __syncthreads();  // the sorted candidates are visible to every thread
     // The row maximum is always a candidate: cand[0] is the argmax (larger
     // value, then smaller id).
-    const uint32_t amax = pk_id(cand[0]);
+    const uint32_t amax = pk_id(fl.cand[0]);
 
     // ---- outputs in raw order (wave 1, while wave 0 draws) ----------------
     // Raw values come from the keys (exact for every value but +-0, whose
@@ -2492,20 +2495,20 @@ __global__ __launch_bounds__(NT) void smp_row(SmpArgs A) {
     if (A.top8_ids && ot >= 0 && ot < 8) {
       const int i = ot;
       const bool in = i < ncand;
-      A.top8_ids[(int64_t)row * 8 + i] = in ? pk_id(cand[i]) : 0xffffffffu;
-      A.top8_vals[(int64_t)row * 8 + i] = in ? raw_value(cand[i]) : -__builtin_inff();
+      A.top8_ids[(int64_t)row * 8 + i] = in ? pk_id(fl.cand[i]) : 0xffffffffu;
+      A.top8_vals[(int64_t)row * 8 + i] = in ? raw_value(fl.cand[i]) : -__builtin_inff();
     }
     if (A.top20_ids && ot >= 0 && ot < 20) {
       const int i = ot;
       const bool in = i < ncand;
-      A.top20_ids[(int64_t)row * 20 + i] = in ? pk_id(cand[i]) : 0xffffffffu;
-      A.top20_vals[(int64_t)row * 20 + i] = in ? raw_value(cand[i]) : -__builtin_inff();
+      A.top20_ids[(int64_t)row * 20 + i] = in ? pk_id(fl.cand[i]) : 0xffffffffu;
+      A.top20_vals[(int64_t)row * 20 + i] = in ? raw_value(fl.cand[i]) : -__builtin_inff();
     }
     if (A.topn_ids && ot >= 0 && ot < A.topn) {
       const int i = ot;
       const bool in = i < ncand;
-      A.topn_ids[(int64_t)row * A.topn + i] = in ? pk_id(cand[i]) : 0xffffffffu;
-      if (A.topn_vals) A.topn_vals[(int64_t)row * A.topn + i] = in ? raw_value(cand[i]) : -__builtin_inff();
+      A.topn_ids[(int64_t)row * A.topn + i] = in ? pk_id(fl.cand[i]) : 0xffffffffu;
+      if (A.topn_vals) A.topn_vals[(int64_t)row * A.topn + i] = in ? raw_value(fl.cand[i]) : -__builtin_inff();
     }
     if (A.n_lp > 0 && ot >= 0 && ot < A.n_lp) {
       const int i = ot;
@@ -2513,10 +2516,10 @@ __global__ __launch_bounds__(NT) void smp_row(SmpArgs A) {
       double lp = -__builtin_inf();
       if (in) {
         // (the sign of a zero does not change l - M)
-        const float l = PEN ? __uint_as_float(value_bits<DT, PEN>(rc, pk_id(cand[i]))) : key2f(pk_key(cand[i]));
+        const float l = PEN ? __uint_as_float(value_bits<DT, PEN>(rc, pk_id(fl.cand[i]))) : key2f(pk_key(fl.cand[i]));
         lp = ((double)l - (double)M) - logZ;
       }
-      A.lp_ids[(int64_t)row * A.n_lp + i] = in ? pk_id(cand[i]) : 0xffffffffu;
+      A.lp_ids[(int64_t)row * A.n_lp + i] = in ? pk_id(fl.cand[i]) : 0xffffffffu;
       A.lp_vals[(int64_t)row * A.n_lp + i] = lp;
     }
     if (A.nll_targets && ot == 0) {
@@ -2547,10 +2550,10 @@ __global__ __launch_bounds__(NT) void smp_row(SmpArgs A) {
           int c = (int)plan.k_eff < (int)ncand ? (int)plan.k_eff : (int)ncand;
           if (plan.need_rel) {
             const uint32_t trel = relevance_key(M, P.temperature);
-            const int nrel = (int)__popcll(__ballot(lane < ncand && pk_key(cand[lane < ncand ? lane : 0]) >= trel));
+            const int nrel = (int)__popcll(__ballot(lane < ncand && pk_key(fl.cand[lane < ncand ? lane : 0]) >= trel));
             c = (int)plan.k_eff < nrel ? (int)plan.k_eff : nrel;
           }
-          sample_tail_wave(A, P, row, cand, c, s_pos, fl.w, have_pre && !dense);
+          sample_tail_wave(A, P, row, fl.cand, c, s_pos, fl.w, have_pre && !dense);
         }
       } else {
         int64_t c;
