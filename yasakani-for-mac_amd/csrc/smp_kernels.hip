@@ -981,7 +981,7 @@ __device__ int64_t dense_compact(const RowCtx& rc, int V, uint32_t theta, uint64
 // it in the LDS tile buffer, which is then written out in order: a digit's
 // entries of the tile are one contiguous run of the destination.
 // lds: 5,888 words; sbuf: NT * 8 entries. Block-wide.
-__device__ void lsd_sort_desc(uint64_t* a, uint64_t* b, int64_t n, uint32_t* lds, uint64_t* sbuf) {
+__device__ __forceinline__ void lsd_sort_desc(uint64_t* a, uint64_t* b, int64_t n, uint32_t* lds, uint64_t* sbuf) {
   constexpr int PER = 8;
   constexpr int64_t TILE = (int64_t)NT * PER;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
