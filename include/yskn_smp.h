@@ -108,7 +108,7 @@ typedef struct yskn_smp_aux {
   /* EXTENSION: the n_logprobs highest raw logits with their logprobs
    * l - max - log(sum_v exp(l_v - max)) in binary64 (the negated
    * negative_log_likelihood of output_head_sampler.rs:230-250). */
-  int32_t n_logprobs;    /* 0..64 */
+  int32_t n_logprobs;    /* 0..vocab (above 64: the row takes the exact dense path) */
   uint32_t* logprob_ids; /* [rows*n_logprobs] */
   double* logprobs;      /* [rows*n_logprobs] */
   int32_t* row_status;   /* [rows] per-row YSKN_SMP_* status */
@@ -247,9 +247,12 @@ int yskn_smp_sample_head(yskn_smp_handle h, const yskn_smp_head* head, int32_t r
 int yskn_smp_argmax(yskn_smp_handle h, const void* logits, int32_t dtype, int32_t rows,
                     int32_t vocab, int64_t ld, uint32_t* out_ids, void* stream);
 
-/* The `count` (<= 64) highest raw logits per row in (value desc, id asc)
+/* The `count` (1..vocab) highest raw logits per row in (value desc, id asc)
  * order: top_tokens() (output_head_sampler.rs:115-134), launch_topk8
- * (src/args.hpp:43-45; src/misc_kernels.cu:100-147). */
+ * (src/args.hpp:43-45; src/misc_kernels.cu:100-147). Counts above 64 take
+ * the exact dense path (the count-th key by radix selection over the row,
+ * then a stable sort of the elements at or above it in the handle's scratch):
+ * correct for any count, slower. */
 int yskn_smp_top_tokens(yskn_smp_handle h, const void* logits, int32_t dtype, int32_t rows,
                         int32_t vocab, int64_t ld, int32_t count, uint32_t* out_ids,
                         float* out_vals, void* stream);

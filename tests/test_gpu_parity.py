@@ -245,6 +245,51 @@ def test_penalties_small(small_dev):
         assert np.array_equal(out["top20_vals"][r].cpu().numpy().view(np.uint32), y[tt].view(np.uint32))
 
 
+@pytest.mark.parametrize("V,count", [(5000, 65), (5000, 1000), (5000, 5000), (70_000, 4097), (70_000, 20_000)])
+def test_top_tokens_beyond_64(small_dev, V, count):
+    # counts above the waves' lists take the exact dense path: every id in
+    # order, ties to the smaller id, raw values (the sign of zeros kept)
+    rng = np.random.default_rng(count + V)
+    x = (2 * rng.standard_normal((3, V))).astype(np.float32)
+    x[1] = np.round(x[1])                                   # heavy ties
+    x[2, : V // 2] = -0.0
+    x[2, V // 2:] = 0.0
+    x[2, 7] = 1.5
+    xt = torch.from_numpy(x).to(DEV)
+    ids, vals = small_dev.top_tokens(xt, count)
+    small_dev.sync()
+    got = to_u32(ids)
+    gv = vals.cpu().numpy()
+    for r in range(3):
+        tt = O.top_tokens(x[r], count)
+        assert np.array_equal(got[r], tt), r
+        assert np.array_equal(gv[r].view(np.uint32), x[r][tt].view(np.uint32)), r
+    with pytest.raises(InvalidInput):
+        small_dev.top_tokens(xt, V + 1)
+
+
+@pytest.mark.parametrize("n_lp,top_k", [(65, 20), (300, 0), (1000, 40)])
+def test_logprobs_beyond_64_keep_the_draw(n_lp, top_k):
+    rng = np.random.default_rng(n_lp)
+    V, rows = 30_000, 4
+    x = (rng.standard_normal((rows, V)) * np.array([[0.5], [1.0], [3.0], [8.0]])).astype(np.float32)
+    sp = SamplingParameters(temperature_milli=900, top_p_milli=930, top_k=top_k, seed=4)
+    d = DeviceSampler(rows, V, extended_top_k=True)
+    d.set_params(sp)
+    pos = np.arange(rows) + 11
+    out = _run(d, torch.from_numpy(x).to(DEV), pos, n_logprobs=n_lp, top20=True)
+    ids = to_u32(out["ids"]).reshape(-1)
+    got_ids = to_u32(out["logprob_ids"])
+    got_lp = out["logprobs"].cpu().numpy()
+    for r in range(rows):
+        assert ids[r] == oracle_select(x[r], int(pos[r]), sp, extension=True), r
+        li, lv = O.top_logprobs(x[r], n_lp)
+        assert list(got_ids[r]) == list(li), r
+        assert_logprobs_close(got_lp[r], lv)
+        assert list(to_u32(out["top20_ids"])[r]) == list(O.top_tokens(x[r], 20))
+    d.close()
+
+
 def test_penalties_across_vocabulary_windows():
     # the history's membership words are built 262,144 ids at a time: ids on
     # both sides of each window edge, the first and last id, one id repeated

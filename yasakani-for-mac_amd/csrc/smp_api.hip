@@ -331,8 +331,8 @@ int apply_aux(yskn_smp_handle h, SmpArgs& a, const yskn_smp_aux* aux, int32_t ro
     if (any_penalty(h, rows)) return fail(YSKN_SMP_EINVAL, "invalid input: penalties need a history");
     return YSKN_SMP_OK;
   }
-  if (aux->n_logprobs < 0 || aux->n_logprobs > KBMAX)
-    return fail(YSKN_SMP_EINVAL, "invalid input: n_logprobs must be in 0..=64");
+  if (aux->n_logprobs < 0 || aux->n_logprobs > a.V)
+    return fail(YSKN_SMP_EINVAL, "invalid input: n_logprobs must be in 0..=vocab");
   if (aux->n_logprobs > 0 && (!aux->logprob_ids || !aux->logprobs))
     return fail(YSKN_SMP_EINVAL, "invalid input: n_logprobs > 0 needs both output arrays");
   if ((aux->top8_ids == nullptr) != (aux->top8_vals == nullptr) ||
@@ -591,7 +591,7 @@ int yskn_smp_top_tokens(yskn_smp_handle h, const void* logits, int32_t dtype, in
                         float* out_vals, void* stream) {
   int st = check_common(h, logits, dtype, rows, vocab, ld);
   if (st) return st;
-  if (count < 1 || count > KBMAX) return fail(YSKN_SMP_EINVAL, "invalid input: count must be in 1..=64");
+  if (count < 1) return fail(YSKN_SMP_EINVAL, "invalid input: count must be at least 1");
   if (count > vocab) return fail(YSKN_SMP_EINVAL, "invalid input: top-token count exceeds vocabulary");
   if (!out_ids) return fail(YSKN_SMP_EINVAL, "invalid input: null output");
   SmpArgs a = base_args(h, logits, rows, vocab, ld);

@@ -394,6 +394,8 @@ __device__ __forceinline__ bool nonfinite_bits(uint32_t b) { return (b & 0x7f800
 struct RowPlan {
   int64_t k_eff;  // candidates of top-k (V when disabled)
   int KB;         // length of the raw-order prefix the row needs
+  int KL;         // length of the waves' lists in the stream: min(KB, KBMAX); a
+                  // row with KB > KBMAX takes the dense path (exact KB-th key)
   bool need_rel;  // large-k sampling: needs every relevant element
   bool sampled;   // not greedy and ids requested
 };
@@ -410,6 +412,7 @@ __device__ __forceinline__ RowPlan make_plan(const SmpArgs& A, const DevParams& 
   if (A.n_lp > kb) kb = A.n_lp;
   if (kb > A.V) kb = A.V;
   p.KB = kb;
+  p.KL = kb < KBMAX ? kb : KBMAX;
   p.need_rel = p.sampled && p.k_eff > KBMAX;
   return p;
 }
@@ -1867,6 +1870,9 @@ __global__ __launch_bounds__(NT) void smp_row(SmpArgs A) {
   __builtin_amdgcn_sched_barrier(0);  // both chunks in flight before any other work
   const DevParams P = A.prm[A.prm_shared ? 0 : row];
   const RowPlan plan = make_plan(A, P);
+  // the exact dense path from the start: forced, or a prefix longer than the
+  // waves' lists (top-N or logprob counts above KBMAX)
+  const bool fdense = A.force_dense != 0 || plan.KB > KBMAX;
   uint32_t wflags = 0;
   const RowCtx rc = make_rowctx<PEN>(A, P, row, ES, &wflags);
   if (tid == 0) {
@@ -1902,7 +1908,7 @@ __global__ __launch_bounds__(NT) void smp_row(SmpArgs A) {
   uint32_t lst = 0u, theta_w = 0u, q_pub = 0u, th_row = 0u;
   uint32_t thr_mk = 0u, thr_th = 0u, thr_c = 1u;  // the last row threshold and its inputs
   uint32_t theta_pub = 0u;                          // theta_w as last published
-  const int qidx = (plan.KB + NW - 1) / NW - 1;
+  const int qidx = (plan.KL + NW - 1) / NW - 1;
   // per chunk: up to its two largest lane maxima enter the list. Each entry
   // costs a wave-wide reduction on the stream's critical path (the waves'
   // first chunks at the start most of all). Early on the list is short, so
@@ -1914,8 +1920,8 @@ __global__ __launch_bounds__(NT) void smp_row(SmpArgs A) {
   // A segmented row gives each wave about one chunk: its first chunk then
   // inserts all its KB largest lane maxima, so that a certified bound exists
   // at once (otherwise the segment would export every element).
-  const int r_next = plan.KB < 2 ? plan.KB : 2;
-  const int r_first = nseg > 1 ? plan.KB : r_next;
+  const int r_next = plan.KL < 2 ? plan.KL : 2;
+  const int r_first = nseg > 1 ? plan.KL : r_next;
 
   // Below lo_f nothing can matter to this wave: no lane maximum would enter
   // its list (lo_f <= its KB-th value), no value would be a candidate
@@ -1963,17 +1969,17 @@ __global__ __launch_bounds__(NT) void smp_row(SmpArgs A) {
           const uint32_t got = (uint32_t)__builtin_amdgcn_ds_permute((int)((put ? rank : 63u) * 4u), (int)lk);
           const int nput = __popcll(in) < rr ? __popcll(in) : rr;
           lst = lane < nput ? got : 0u;
-          theta_w = (uint32_t)__builtin_amdgcn_readlane((int)lst, plan.KB - 1);
+          theta_w = (uint32_t)__builtin_amdgcn_readlane((int)lst, plan.KL - 1);
         } else {
           for (int i = 0; i < rr; ++i) {
             const uint32_t m = wave_max_dpp(rk);
             if (i == 0) cmax = m;
             if (m <= theta_w || m <= th_row) break;  // 0, cannot enter the full list, or below the row bound
             // insert m: entries >= m keep their lanes, the rest move up by one
-            const uint32_t pos = (uint32_t)__popcll(__ballot(lane < plan.KB && lst >= m));
+            const uint32_t pos = (uint32_t)__popcll(__ballot(lane < plan.KL && lst >= m));
             const uint32_t up = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)lst, 0x138, 0xf, 0xf, false);  // wave_shr:1
             lst = (uint32_t)lane < pos ? lst : ((uint32_t)lane == pos ? m : up);
-            theta_w = (uint32_t)__builtin_amdgcn_readlane((int)lst, plan.KB - 1);
+            theta_w = (uint32_t)__builtin_amdgcn_readlane((int)lst, plan.KL - 1);
             const uint64_t eq = __ballot(rk == m);
             if (lane == (int)__builtin_ctzll(eq)) rk = 0u;
           }
@@ -2026,13 +2032,13 @@ __global__ __launch_bounds__(NT) void smp_row(SmpArgs A) {
       if (mk != thr_mk || th != thr_th) {
         thr_mk = mk;
         thr_th = th;
-        thr_c = A.force_dense ? 0xffffffffu : row_threshold(plan, P, key2f(mk), th);
+        thr_c = fdense ? 0xffffffffu : row_threshold(plan, P, key2f(mk), th);
       }
       const uint32_t thr = thr_c;
       // (a wave's first chunk has about KB lanes with survivors by
       // construction -- the lane maxima that set its first bound -- so its
       // deferral limit is raised by KB)
-      chunk_filter<DT>(c, lane, X, thr, mk, A.want_mass != 0, lk, cmax, first ? DLANES + plan.KB : DLANES, ws,
+      chunk_filter<DT>(c, lane, X, thr, mk, A.want_mass != 0, lk, cmax, first ? DLANES + plan.KL : DLANES, ws,
                        sh, fl, spill);
       th_row = th;
       const float lo_list = key_threshold_float(theta_w > th ? theta_w : th);
@@ -2091,7 +2097,7 @@ __global__ __launch_bounds__(NT) void smp_row(SmpArgs A) {
   // the best single-wave bound: no bound used in the stream exceeds the
   // final one (every improvement was published), which keeps the buffer
   // complete down to it.
-  if (lane < 8) fl.lists[wave * 8 + lane] = lane < plan.KB ? lst : 0u;
+  if (lane < 8) fl.lists[wave * 8 + lane] = lane < plan.KL ? lst : 0u;
   // The wave's own results, which the deferred chunks below do not change
   // (they add no mass terms and find no new maximum).
   if (__ballot(ws.bad)) wflags |= F_NONFINITE;
@@ -2107,7 +2113,7 @@ __global__ __launch_bounds__(NT) void smp_row(SmpArgs A) {
   // every wave ranks the union itself (the same value in all): no second barrier
   uint32_t theta = sh.bw[BW_THETA];
   {
-    const uint32_t t = wave_kth_largest_radix(fl.lists[lane], plan.KB);
+    const uint32_t t = wave_kth_largest_radix(fl.lists[lane], plan.KL);
     theta = t > theta ? t : theta;
   }
   // Deferred chunks against the final bound: one whose second largest key
@@ -2115,7 +2121,7 @@ __global__ __launch_bounds__(NT) void smp_row(SmpArgs A) {
   // its largest does hands that element over directly (wave 0); the rest
   // hold nothing at or above it. Entry i is read again by wave i % NW; each
   // wave keeps two of its chunks in flight (the stream's buffers are free).
-  if (!A.force_dense) {
+  if (!fdense) {
     const uint32_t mkf = sh.bw[BW_MKEY];
     const uint32_t thr_f = row_threshold(plan, P, key2f(mkf), theta);
     const uint32_t nd = sh.ndef < (uint32_t)DEFCAP ? sh.ndef : (uint32_t)DEFCAP;
@@ -2203,7 +2209,7 @@ __global__ __launch_bounds__(NT) void smp_row(SmpArgs A) {
   int n_mass = NW;  // mass terms in s_mref / s_mass
   if (nseg > 1) {
     const uint32_t mk_s = sh.bw[BW_MKEY];
-    const uint32_t theta_s = A.force_dense ? 0xffffffffu : row_threshold(plan, P, key2f(mk_s), theta);
+    const uint32_t theta_s = fdense ? 0xffffffffu : row_threshold(plan, P, key2f(mk_s), theta);
     uint64_t* const xc = A.exp_cand + ((int64_t)row * nseg + seg) * EXP_CAP;
     const uint32_t cnt = sh.count;
     uint32_t nx;
@@ -2359,7 +2365,7 @@ __global__ __launch_bounds__(NT) void smp_row(SmpArgs A) {
     // or above theta_f are exactly the row's: sorted, they hold the top-KB
     // and every relevant element, which is all the outputs and the tail read.
     const uint32_t theta_f = row_threshold(plan, P, M, theta);
-    bool dense = A.force_dense != 0 || (P.zcheck && plan.sampled);
+    bool dense = fdense || (P.zcheck && plan.sampled);
     bool zfail = false;
     int64_t ncand = 0;
     bool sorted = false;
@@ -2480,8 +2486,10 @@ __global__ __launch_bounds__(NT) void smp_row(SmpArgs A) {
     const int ot = tid - 64;  // wave 1's lanes: 0..63
     // log of the mass (wave 1 alone, off the draw's path): one term per
     // wave, in lanes 0..NW-1
+    // (more than 64 outputs: every wave writes them, and needs logZ)
+    const bool big_out = A.topn > 64 || A.n_lp > 64;
     double logZ = 0.0;
-    if (A.want_mass && wave == 1) {
+    if (A.want_mass && (wave == 1 || big_out)) {
       double t = 0.0;
       if (lane < n_mass && s_mref[lane] != -__builtin_inff()) t = s_mass[lane] * exp((double)s_mref[lane] - (double)M);
       logZ = log(wave_sum_f64_dpp(t));
@@ -2504,13 +2512,30 @@ __global__ __launch_bounds__(NT) void smp_row(SmpArgs A) {
       A.top20_ids[(int64_t)row * 20 + i] = in ? pk_id(fl.cand[i]) : 0xffffffffu;
       A.top20_vals[(int64_t)row * 20 + i] = in ? raw_value(fl.cand[i]) : -__builtin_inff();
     }
-    if (A.topn_ids && ot >= 0 && ot < A.topn) {
+    if (A.topn_ids && A.topn > 64) {
+      for (int64_t i = tid; i < A.topn; i += NT) {
+        const bool in = i < ncand;
+        A.topn_ids[(int64_t)row * A.topn + i] = in ? pk_id(cand[i]) : 0xffffffffu;
+        if (A.topn_vals) A.topn_vals[(int64_t)row * A.topn + i] = in ? raw_value(cand[i]) : -__builtin_inff();
+      }
+    } else if (A.topn_ids && ot >= 0 && ot < A.topn) {
       const int i = ot;
       const bool in = i < ncand;
       A.topn_ids[(int64_t)row * A.topn + i] = in ? pk_id(fl.cand[i]) : 0xffffffffu;
       if (A.topn_vals) A.topn_vals[(int64_t)row * A.topn + i] = in ? raw_value(fl.cand[i]) : -__builtin_inff();
     }
-    if (A.n_lp > 0 && ot >= 0 && ot < A.n_lp) {
+    if (A.n_lp > 64) {
+      for (int64_t i = tid; i < A.n_lp; i += NT) {
+        const bool in = i < ncand;
+        double lp = -__builtin_inf();
+        if (in) {
+          const float l = PEN ? __uint_as_float(value_bits<DT, PEN>(rc, pk_id(cand[i]))) : key2f(pk_key(cand[i]));
+          lp = ((double)l - (double)M) - logZ;
+        }
+        A.lp_ids[(int64_t)row * A.n_lp + i] = in ? pk_id(cand[i]) : 0xffffffffu;
+        A.lp_vals[(int64_t)row * A.n_lp + i] = lp;
+      }
+    } else if (A.n_lp > 0 && ot >= 0 && ot < A.n_lp) {
       const int i = ot;
       const bool in = i < ncand;
       double lp = -__builtin_inf();

@@ -237,7 +237,7 @@ inline Result<uint32_t> greedy(const std::vector<float>& logits) {
 }
 
 // top_tokens (output_head_sampler.rs:115-134): the first `count` ids in
-// (logit desc, id asc) order; count <= 64 on this device path.
+// (logit desc, id asc) order, any count up to the vocabulary.
 inline Result<std::vector<uint32_t>> top_tokens(const std::vector<float>& logits, size_t count) {
   if (!detail::vocabulary_ok(logits.size()))
     return detail::invalid("invalid input: logits must contain a nonempty u32-indexed vocabulary");
