@@ -212,6 +212,42 @@ def test_sample_at_advance_runs_a_decode_loop_on_the_device():
     d.close()
 
 
+def test_decode_step_replays_in_a_hip_graph():
+    # the decode step (device position form, device advance, a row split in
+    # segments) captured once in a HIP graph: the call allocates nothing and
+    # records no memset, so every replay samples at the advanced position
+    # exactly as an eager call does; eager work and synchronisation between
+    # the replays
+    rng = np.random.default_rng(43)
+    V = 30_000
+    x = (2.5 * rng.standard_normal((1, V))).astype(np.float32)
+    xt = torch.from_numpy(x).to(DEV)
+    d = DeviceSampler(1, V)
+    sp = SamplingParameters(temperature_milli=800, top_p_milli=950, top_k=20, seed=91)
+    d.set_params(sp)
+    pos = torch.tensor([900], dtype=torch.int64, device=DEV)
+    tok = torch.full((1,), -1, dtype=torch.int32, device=DEV)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        out = d.sample_at(xt, pos, advance=(pos, tok), top20=True)
+    assert int(pos.cpu()[0]) == 900                 # capture runs nothing
+    for r in range(6):
+        g.replay()
+        d.sync()
+        p = 900 + r + 1
+        assert int(pos.cpu()[0]) == p
+        want = oracle_select(x[0], p, sp)
+        assert int(tok.cpu()[0]) == want and int(out["ids"].cpu()[0]) == want
+        assert list(to_u32(out["top20_ids"])[0]) == list(O.top_tokens(x[0], 20))
+        # eager work between replays: a torch reduction and an eager call
+        assert float((xt * 2.0).sum()) == pytest.approx(2.0 * float(xt.sum()), rel=1e-5)
+        e = d.sample(xt, torch.tensor([[p]], dtype=torch.int64, device=DEV))
+        d.sync()
+        assert int(to_u32(e["ids"])[0, 0]) == want
+    d.close()
+
+
 def test_sample_at_position_overflow_fails_the_row():
     V = 1000
     x = torch.zeros((2, V), dtype=torch.float32, device=DEV)
