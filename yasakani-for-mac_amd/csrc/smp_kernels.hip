@@ -2697,12 +2697,13 @@ __global__ __launch_bounds__(PP_NT) void smp_penalty_prep(PenArgs A) {
   __shared__ uint32_t red[PP_NT / 64];
   __shared__ int s_bad;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, row = blockIdx.x;
+  // (the parameters and the length are requested together: one round trip)
   const DevParams P = A.prm[A.prm_shared ? 0 : row];
+  const int len = A.history_len ? A.history_len[row] : 0;
   if (!P.penalize) {
     if (tid == 0) A.len[row] = 0;
     return;
   }
-  const int len = A.history_len ? A.history_len[row] : 0;
   if (len < 0 || len > HCAP || (A.history_ld > 0 && (int64_t)len > A.history_ld)) {
     if (tid == 0) A.len[row] = -1;
     return;
