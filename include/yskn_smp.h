@@ -362,8 +362,8 @@ int yskn_smp_select_host(yskn_smp_handle h, const float* host_logits, int32_t vo
 /* Profiling counters of the handle, cumulative since create (no counterpart
  * in the reference, which has no sampler-level instrumentation): out[0] rows
  * finished, out[1] rows served by the exact large-candidate path, out[2]
- * reserved (0), out[3] candidates sorted by the row blocks. Synchronises the
- * device.
+ * those of them whose cut was certified without sorting the row, out[3]
+ * candidates sorted by the row blocks. Synchronises the device.
  * Returns the number of counters written (<= n) or a negative status. */
 int yskn_smp_get_stats(yskn_smp_handle h, uint64_t* out, int32_t n);
 

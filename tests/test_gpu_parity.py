@@ -364,6 +364,92 @@ def test_dense_path_matches_compact_path():
     b.close()
 
 
+def _dense_rows(rng, rows, V, dtype=np.float32):
+    scale = np.array([0.5, 1.0, 2.0, 3.0])[np.arange(rows) % 4].reshape(-1, 1)
+    return (scale * rng.standard_normal((rows, V))).astype(dtype)
+
+
+def _dense_params(rows, seed):
+    """Top-k disabled; temperatures, top-p and min-p that put the cut before
+    and after min-p's, at top-p 1 (no margin: the sorting path) and at
+    min-p 0."""
+    Ts = [300, 700, 1000, 1500]
+    tps = [800, 900, 950, 990, 1000]
+    mps = [0, 1, 20, 100, 0, 3]
+    return [SamplingParameters(temperature_milli=Ts[r % 4], top_p_milli=tps[r % 5], min_p_milli=mps[r % 6],
+                               top_k=0, seed=seed + r) for r in range(rows)]
+
+
+def test_certified_dense_tail_matches_the_oracle_and_the_sorting_path():
+    """Rows with tens of thousands of candidates (top-k disabled): the cut is
+    certified from bucket sums without sorting the row, or the row falls back
+    to the sort. Both give the oracle's ids; the forced sorting path agrees."""
+    rng = np.random.default_rng(41)
+    rows, V = 24, 50_000
+    x = _dense_rows(rng, rows, V)
+    sps = _dense_params(rows, 900)
+    a = DeviceSampler(rows, V, extended_top_k=True)
+    b = DeviceSampler(rows, V, extended_top_k=True, force_dense=True)
+    a.set_params(sps)
+    b.set_params(sps)
+    pos = np.arange(rows) + 123
+    xt = torch.from_numpy(x).to(DEV)
+    oa = _run(a, xt, pos, argmax=True, top20=True, n_logprobs=8)
+    ob = _run(b, xt, pos, argmax=True, top20=True, n_logprobs=8)
+    ref = pmap(lambda r: oracle_select(x[r], int(pos[r]), sps[r], extension=True), range(rows))
+    assert list(to_u32(oa["ids"]).reshape(-1)) == ref
+    for key in ("ids", "argmax", "top20_ids", "logprob_ids"):
+        assert torch.equal(oa[key], ob[key]), key
+    st = a.stats()
+    assert st["dense_rows"] == rows
+    assert 0 < st["certified_rows"] < rows  # top-p 1 at min-p 0 has no margin: sorted
+    a.close()
+    b.close()
+
+
+def test_certified_dense_tail_several_draws_and_ties():
+    """Several positions per row, and bf16 rows whose values repeat (the cut
+    falls inside a run of equal values: ids in ascending order decide)."""
+    rng = np.random.default_rng(42)
+    rows, V, nd = 8, 60_000, 5
+    x = _dense_rows(rng, rows, V)
+    xb = torch.from_numpy(x).to(torch.bfloat16)
+    xf = xb.float().numpy()
+    sps = _dense_params(rows, 300)
+    d = DeviceSampler(rows, V, extended_top_k=True)
+    d.set_params(sps)
+    pos = (np.arange(rows * nd).reshape(rows, nd) * 7 + 11).astype(np.int64)
+    out = _run(d, xb.to(DEV), pos)
+    got = to_u32(out["ids"]).reshape(rows, nd)
+    for r in range(rows):
+        ref = O.sample_positions(xf[r], pos[r].astype(np.uint64), oracle_params(sps[r], True))
+        assert list(got[r]) == list(ref), r
+    assert d.stats()["certified_rows"] > 0
+    d.close()
+
+
+def test_certified_dense_tail_with_penalties_and_coarse_values():
+    """Penalised rows, and rows of a few distinct values (a cut bucket too
+    large to collect: the sorting path)."""
+    rng = np.random.default_rng(43)
+    rows, V = 6, 40_000
+    x = _dense_rows(rng, rows, V)
+    x[3:] = np.round(x[3:] * 4) / 4
+    hist = rng.integers(0, V, (rows, 3000)).astype(np.int32)
+    sps = _dense_params(rows, 50)
+    sps = [SamplingParameters(temperature_milli=s.temperature_milli, top_p_milli=s.top_p_milli,
+                              min_p_milli=s.min_p_milli, top_k=0, seed=s.seed, repetition_penalty=1.1,
+                              presence_penalty=0.2, frequency_penalty=0.05) for s in sps]
+    d = DeviceSampler(rows, V, extended_top_k=True)
+    d.set_params(sps)
+    pos = np.arange(rows) + 5
+    out = _run(d, torch.from_numpy(x).to(DEV), pos, history=torch.from_numpy(hist).to(DEV))
+    for r in range(rows):
+        y = O.apply_penalties(x[r], hist[r], 1.1, 0.2, 0.05)
+        assert to_u32(out["ids"])[r, 0] == oracle_select(y, int(pos[r]), sps[r], extension=True), r
+    d.close()
+
+
 # ---------------------------------------------------------------------------
 # the five workloads at full size
 # ---------------------------------------------------------------------------
@@ -439,6 +525,9 @@ def test_batched_heterogeneous():
     ref = pmap(lambda r: oracle_select(xn[r], int(pos[r]), sps[r], extension=True), range(64))
     assert list(to_u32(out["ids"]).reshape(-1)) == ref
     assert list(to_u32(out["argmax"])) == [int(np.argmax(xn[r])) for r in range(64)]
+    st = d.stats()
+    print("path counters", st, flush=True)
+    assert st["dense_rows"] == 16 and st["certified_rows"] == 16  # the top-k-disabled rows
     d.close()
 
 

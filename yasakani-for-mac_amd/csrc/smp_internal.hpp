@@ -76,7 +76,7 @@ struct SegMeta {
 enum StatIndex {
   STAT_ROWS = 0,      // rows finished
   STAT_DENSE_ROWS,    // rows served by the exact large-candidate path
-  STAT_RESCAN_WAVES,  // always 0 (kept for the counter layout of the C ABI)
+  STAT_CERT_ROWS,     // of those, rows whose cut was certified without a sort
   STAT_CANDIDATES,    // candidates sorted by the row blocks
   STAT_COUNT
 };

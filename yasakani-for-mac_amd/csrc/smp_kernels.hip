@@ -942,10 +942,16 @@ __device__ int64_t dense_compact(const RowCtx& rc, int V, uint32_t theta, uint64
   for (int64_t base = 0; base < V; base += (int64_t)NT * PER) {
     uint32_t keys[PER];
     uint64_t m[PER];
+    // every load issued (clamped index) so that all PER are in flight together
 #pragma unroll
     for (int q = 0; q < PER; ++q) {
       const int64_t i = base + (int64_t)q * NT + tid;
-      keys[q] = i < V ? f2key(value_bits<DT, PEN>(rc, i)) : 0u;
+      keys[q] = value_bits<DT, PEN>(rc, i < V ? i : (int64_t)V - 1);
+    }
+#pragma unroll
+    for (int q = 0; q < PER; ++q) {
+      const int64_t i = base + (int64_t)q * NT + tid;
+      keys[q] = i < V ? f2key(keys[q]) : 0u;
     }
 #pragma unroll
     for (int q = 0; q < PER; ++q) {
@@ -1810,6 +1816,480 @@ __device__ __forceinline__ uint32_t compact_entries(const uint64_t* src, uint32_
 }
 
 // ---------------------------------------------------------------------------
+// The tail of a large-candidate row without sorting the row (top-k disabled
+// or above the relevant count, version 3, lists of at most KBMAX entries).
+//
+// The reference sorts the candidates, forms w_j = exp_d(z_j), cuts at the
+// first serial binary64 prefix S_j >= top_p * total and at the first w_j
+// below min-p, and draws over the kept prefix (output_head_sampler.rs
+// :136-190). Only the cut needs the order, and only near it:
+//  1. one pass over the row adds every relevant weight, and a count, into
+//     one of CB_NB buckets of z (bucket b holds the z with
+//     floor(-z CB_NB / 37.5) = b, the last bucket everything below: an
+//     interval of the candidate order), and finds the largest key whose
+//     weight is below min-p (the first candidate min-p drops);
+//  2. a second pass collects the bucket in which the running bucket sums
+//     cross top_p * total and the buckets that hold the first KB candidates
+//     (the lists), and sums the weights of the min-p bucket's kept
+//     candidates; both collections are sorted in LDS;
+//  3. the sums are not the reference's serial binary64 sum: other order,
+//     weights from exp_approx of z' = (l - M) * (1 / T) instead of exp_d of
+//     z = (l - M) / T (within 2^-44 of w each for |z| <= 40). Every prefix
+//     or total formed here is within
+//     E = 2^-53 R (4n + 2 CB_NB + 2 CAP + 64) + 2^-43 R
+//     of the serial value it stands for (R the total, n the candidates:
+//     each serial addition, each bucket and scan addition, each addition of
+//     the walk through the collected bucket and the top-p product round by
+//     at most 2^-53 R; the weights add at most 2^-44 R). A cut is taken only
+//     when every compare it rests on holds with a margin of 2E, and min-p's
+//     only when no weight lies within 2^-40 of min-p (relative); otherwise,
+//     or when a collection does not fit, the function returns 0 and the
+//     caller sorts the row (the exact path);
+//  4. the kept candidates are a prefix of the order: every element with key
+//     above the cut key and, at the cut key, the ids up to the cut id. They
+//     are compacted; a draw takes the largest binary32 score (within
+//     SC_TOL of z + g, score_approx) over them, then the exact binary64
+//     z + g of the entries within 2 SC_TOL of it, ties to the earlier
+//     candidate (the reference's strict > in candidate order).
+// Passes over the row keep the next tile's loads in flight while a tile is
+// processed. On success fl.cand holds the first KB candidates, sorted,
+// out_ids the draws, and the return value is the number of relevant
+// elements. Block-wide.
+// ---------------------------------------------------------------------------
+constexpr int CB_NB = 4096;     // z buckets of the certified tail
+constexpr float SC_TOL = 1e-4f;  // bound on |score_approx - (z + g)|
+constexpr int DRB = 8;           // entries per thread and round of the draw passes
+
+__device__ __forceinline__ uint32_t cert_bucket(double z) {
+  const double t = -z * ((double)CB_NB / 37.5);
+  return t < (double)(CB_NB - 1) ? (uint32_t)t : (uint32_t)(CB_NB - 1);
+}
+
+// e^z for z <= 0 within 2^-50 (relative): Cody-Waite reduction by ln 2 with
+// fused multiply-adds, a degree-13 Taylor polynomial on |r| <= 0.35
+// (truncation below 2^-57), the power of two set in the exponent field.
+// Not the reference's exp_d: used only where its error is bounded above.
+__device__ __forceinline__ double exp_approx(double z) {
+  z = z >= -700.0 ? z : -700.0;  // (a NaN, from a padding lane, too: every value below stays defined)
+  const double t = __builtin_rint(z * 1.4426950408889634);
+  double r = __builtin_fma(-t, 0.6931471805599453, z);
+  r = __builtin_fma(-t, 2.3190468138462996e-17, r);
+  double p = 1.6059043836821613e-10;          // 1/13!
+  p = __builtin_fma(p, r, 2.08767569878681e-09);   // 1/12!
+  p = __builtin_fma(p, r, 2.505210838544172e-08);  // 1/11!
+  p = __builtin_fma(p, r, 2.755731922398589e-07);  // 1/10!
+  p = __builtin_fma(p, r, 2.7557319223985893e-06); // 1/9!
+  p = __builtin_fma(p, r, 2.48015873015873e-05);   // 1/8!
+  p = __builtin_fma(p, r, 0.0001984126984126984);  // 1/7!
+  p = __builtin_fma(p, r, 0.001388888888888889);   // 1/6!
+  p = __builtin_fma(p, r, 0.008333333333333333);   // 1/5!
+  p = __builtin_fma(p, r, 0.041666666666666664);   // 1/4!
+  p = __builtin_fma(p, r, 0.16666666666666666);    // 1/3!
+  p = __builtin_fma(p, r, 0.5);
+  p = __builtin_fma(p, r, 1.0);
+  p = __builtin_fma(p, r, 1.0);
+  const int64_t k = (int64_t)t;
+  return p * __longlong_as_double((long long)((uint64_t)(k + 1023) << 52));
+}
+
+// z + g of the version-3 draw in binary32 arithmetic, within SC_TOL of the
+// binary64 value for |z| <= 40 and every uniform below 1 (z to ~5e-6; -log u
+// to ~1e-6 relative: from 1 - u, exact in binary64, by a series when u is
+// near 1, else from log of u; the outer log adds ~3e-6; 2.7e-6 is the
+// largest error over 2e7 uniforms, the endpoints included). At the
+// uniform's upper endpoint u = 1 both are +inf: that entry is always
+// evaluated exactly.
+__device__ __forceinline__ float score_approx(float zf, uint64_t pk, uint32_t token) {
+  const uint64_t h = mix64(pk ^ ((uint64_t)token * 0xd6e8feb86659fd93ull));
+  const double u = ((double)(h >> 11) + 0.5) * (1.0 / 9007199254740992.0);  // the reference's uniform
+  const float d = (float)(1.0 - u);  // exact for u >= 1/2
+  float l1;
+  if (d < 0.0625f) {
+    l1 = d * (1.0f + d * (0.5f + d * (0.33333334f + d * (0.25f + d * 0.2f))));
+  } else {
+    l1 = -logf((float)u);
+  }
+  return zf - logf(l1);
+}
+
+struct CertShared {
+  double R;            // sum of the bucket sums
+  double a_cut;        // bucket sums before the cut bucket
+  double a_fb;         // bucket sums before the bucket of the first candidate min-p drops
+  double p_lo, p_hi;   // prefix before and through the cut candidate
+  uint32_t n;          // relevant elements
+  uint32_t bcut, ccut; // cut bucket, candidates before it
+  uint32_t btop, ctop; // last bucket of the head, candidates through it
+  uint32_t ncut, ntop; // entries collected
+  uint32_t nk;         // kept entries compacted
+  int32_t j0;          // cut position in the sorted cut bucket (-1: not found)
+};
+
+// Keys of elements base + q * NT + tid (0 past the row). Every load is
+// issued, at a clamped index, so that all PER are in flight together (a
+// load behind a per-element branch waits for the one before it).
+template <int DT, bool PEN, int PER>
+__device__ __forceinline__ void cert_load(const RowCtx& rc, int V, int64_t base, uint32_t (&k)[PER]) {
+  uint32_t b[PER];
+#pragma unroll
+  for (int q = 0; q < PER; ++q) {
+    const int64_t i = base + (int64_t)q * NT + (int64_t)threadIdx.x;
+    b[q] = value_bits<DT, PEN>(rc, i < V ? i : (int64_t)V - 1);
+  }
+#pragma unroll
+  for (int q = 0; q < PER; ++q) {
+    const int64_t i = base + (int64_t)q * NT + (int64_t)threadIdx.x;
+    k[q] = i < V ? f2key(b[q]) : 0u;
+  }
+}
+
+template <int DT, bool PEN>
+__device__ __forceinline__ int64_t dense_certified(const SmpArgs& A, const DevParams& P, const RowCtx& rc,
+                                                   int row, float M, uint32_t trel, const RowPlan& plan,
+                                                   RowLds& fl, double* redd, uint64_t* redu) {
+  constexpr int P1 = 8, P2 = 16;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int V = A.V;
+  const double T = P.temperature;
+  const double invT = 1.0 / T;
+  const double Md = (double)M;
+  double* hw = (double*)fl.buf;                            // [CB_NB] bucket sums
+  uint32_t* hc = (uint32_t*)(fl.buf + CB_NB);              // [CB_NB] bucket counts
+  CertShared* cs = (CertShared*)(fl.buf + CB_NB + CB_NB / 2);
+  uint64_t* top = fl.cand;                                 // the head buckets
+  uint64_t* cut = (uint64_t*)fl.w;                         // the cut bucket
+  for (int i = tid; i < CB_NB; i += NT) {
+    hw[i] = 0.0;
+    hc[i] = 0u;
+  }
+  if (tid == 0) {
+    cs->ncut = 0u;
+    cs->ntop = 0u;
+    cs->nk = 0u;
+  }
+  __syncthreads();
+  // 1. bucket sums and counts; the largest key whose weight is below min-p
+  const double mp_lo = P.min_p * (1.0 - 0x1p-40), mp_hi = P.min_p * (1.0 + 0x1p-40);
+  uint32_t kfb = 0u;
+  bool amb = false;  // a weight too close to min-p to decide
+  {
+    uint32_t nx[P1];
+    cert_load<DT, PEN, P1>(rc, V, 0, nx);
+    for (int64_t base = 0; base < V; base += (int64_t)NT * P1) {
+      uint32_t kk[P1];
+#pragma unroll
+      for (int q = 0; q < P1; ++q) kk[q] = nx[q];
+      if (base + (int64_t)NT * P1 < V) cert_load<DT, PEN, P1>(rc, V, base + (int64_t)NT * P1, nx);
+#pragma unroll
+      for (int q = 0; q < P1; ++q) {
+        const double z = ((double)key2f(kk[q]) - Md) * invT;
+        const double w = exp_approx(z);
+        if (kk[q] >= trel) {
+          const uint32_t b = cert_bucket(z);
+          atomicAdd(&hw[b], w);
+          atomicAdd(&hc[b], 1u);
+          if (w < mp_lo && kk[q] > kfb) kfb = kk[q];
+          amb |= w >= mp_lo && w <= mp_hi;
+        }
+      }
+    }
+  }
+  kfb = (uint32_t)block_max_u64((uint64_t)kfb, redu);
+  amb = block_max_u64(amb ? 1ull : 0ull, redu) != 0ull;
+  const uint32_t bfb = kfb ? cert_bucket(((double)key2f(kfb) - Md) * invT) : (uint32_t)CB_NB;
+  __syncthreads();
+  // the running sums over the buckets (wave 0; lane l owns buckets 64l..64l+63)
+  if (wave == 0) {
+    const int b0 = lane * 64;
+    double sw = 0.0;
+    uint32_t sc = 0u;
+    for (int i = 0; i < 64; ++i) {
+      sw += hw[b0 + i];
+      sc += hc[b0 + i];
+    }
+    double ew = sw;
+    uint32_t ec = sc;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const double tw = __shfl_up(ew, o);
+      const uint32_t tc = (uint32_t)__shfl_up((int)ec, o);
+      if (lane >= o) {
+        ew += tw;
+        ec += tc;
+      }
+    }
+    const double R = __shfl(ew, 63);
+    const uint32_t n = (uint32_t)__shfl((int)ec, 63);
+    const double tau = P.top_p * R;
+    double a = ew - sw;
+    uint32_t c = ec - sc;
+    int fcut = -1, ftop = -1;
+    double acut = 0.0, afb = 0.0;
+    uint32_t ccut = 0u, ctop = 0u;
+    for (int i = 0; i < 64; ++i) {
+      const double wb = hw[b0 + i];
+      const uint32_t cb = hc[b0 + i];
+      if (fcut < 0 && a + wb >= tau) {
+        fcut = b0 + i;
+        acut = a;
+        ccut = c;
+      }
+      if (ftop < 0 && c + cb >= (uint32_t)plan.KB) {
+        ftop = b0 + i;
+        ctop = c + cb;
+      }
+      if ((uint32_t)(b0 + i) == bfb) afb = a;
+      a += wb;
+      c += cb;
+    }
+    const uint64_t mc = __ballot(fcut >= 0), mt = __ballot(ftop >= 0);
+    const int lc = mc ? (int)__builtin_ctzll(mc) : 0, lt = mt ? (int)__builtin_ctzll(mt) : 0;
+    const int bcut = __shfl(fcut, lc), btop = __shfl(ftop, lt);
+    const double a_cut = __shfl(acut, lc);
+    const uint32_t c_cut = (uint32_t)__shfl((int)ccut, lc), c_top = (uint32_t)__shfl((int)ctop, lt);
+    if ((uint32_t)lane == (bfb >> 6) && bfb < (uint32_t)CB_NB) cs->a_fb = afb;
+    if (lane == 0) {
+      cs->R = R;
+      cs->n = n;
+      cs->bcut = mc ? (uint32_t)bcut : (uint32_t)CB_NB;
+      cs->a_cut = a_cut;
+      cs->ccut = c_cut;
+      cs->btop = mt ? (uint32_t)btop : (uint32_t)CB_NB;
+      cs->ctop = c_top;
+    }
+  }
+  __syncthreads();
+  const uint32_t n = cs->n, bcut = cs->bcut, btop = cs->btop;
+  // the candidates are the relevant elements (top-k at or above their
+  // count); the cut bucket and the head must fit the LDS collections
+  if (amb || n == 0u || plan.k_eff < (int64_t)n || bcut >= (uint32_t)CB_NB || btop >= (uint32_t)CB_NB ||
+      hc[bcut] > (uint32_t)CAP || cs->ctop > (uint32_t)CAP) {
+    __syncthreads();
+    return 0;
+  }
+  // 2. collect the cut bucket and the head; sum what min-p keeps of its bucket
+  double pfb = 0.0;
+  {
+    uint32_t nx[P2];
+    cert_load<DT, PEN, P2>(rc, V, 0, nx);
+    for (int64_t base = 0; base < V; base += (int64_t)NT * P2) {
+      uint32_t kk[P2];
+#pragma unroll
+      for (int q = 0; q < P2; ++q) kk[q] = nx[q];
+      if (base + (int64_t)NT * P2 < V) cert_load<DT, PEN, P2>(rc, V, base + (int64_t)NT * P2, nx);
+#pragma unroll
+      for (int q = 0; q < P2; ++q) {
+        if (kk[q] >= trel) {
+          const double z = ((double)key2f(kk[q]) - Md) * invT;
+          const uint32_t b = cert_bucket(z);
+          const uint64_t e = pack(kk[q], (uint32_t)(base + (int64_t)q * NT + tid));
+          if (b == bfb && kk[q] > kfb) pfb += exp_approx(z);
+          if (b == bcut) {
+            const uint32_t s = atomicAdd(&cs->ncut, 1u);
+            if (s < (uint32_t)CAP) cut[s] = e;
+          }
+          if (b <= btop) {
+            const uint32_t s = atomicAdd(&cs->ntop, 1u);
+            if (s < (uint32_t)CAP) top[s] = e;
+          }
+        }
+      }
+    }
+  }
+  pfb = block_sum_f64(pfb, redd);
+  __syncthreads();
+  const uint32_t ncut = cs->ncut, ntop = cs->ntop;
+  if (ncut != hc[bcut] || ntop != cs->ctop) {
+    __syncthreads();
+    return 0;
+  }
+  __syncthreads();
+  sort_desc(top, (int)ntop);
+  sort_desc(cut, (int)ncut);
+  // the cut bucket's weights, in candidate order
+  for (uint32_t j = (uint32_t)tid; j < ncut; j += NT) hw[j] = exp_approx(((double)key2f(pk_key(cut[j])) - Md) * invT);
+  __syncthreads();
+  // 3. the cut, certified
+  const double R = cs->R;
+  const double marg = 2.0 * ((R * 0x1p-53) * (4.0 * (double)n + 2.0 * CB_NB + 2.0 * CAP + 64.0) + R * 0x1p-43);
+  const double tau = P.top_p * R;
+  int mode = 0;  // 0: not certified, 1: min-p cut, 2: top-p cut
+  if (kfb) {
+    const double pm = cs->a_fb + pfb;  // the weights of the candidates min-p keeps
+    if (pm < tau - marg) mode = 1;
+    else if (pm >= tau + marg) mode = 2;
+  } else {
+    mode = 2;
+  }
+  if (mode == 2) {
+    if (wave == 0) {
+      const uint32_t K = (ncut + 63u) / 64u;
+      const uint32_t j0 = (uint32_t)lane * K;
+      const uint32_t j1 = j0 + K < ncut ? j0 + K : ncut;
+      double s = 0.0;
+      for (uint32_t j = j0; j < j1; ++j) s += hw[j];
+      double e = s;
+#pragma unroll
+      for (int o = 1; o < 64; o <<= 1) {
+        const double t = __shfl_up(e, o);
+        if (lane >= o) e += t;
+      }
+      double run = cs->a_cut + (e - s), lo = 0.0, hi = 0.0;
+      int found = -1;
+      for (uint32_t j = j0; j < j1; ++j) {
+        const double prev = run;
+        run += hw[j];
+        if (found < 0 && run >= tau) {
+          found = (int)j;
+          lo = prev;
+          hi = run;
+        }
+      }
+      const uint64_t mf = __ballot(found >= 0);
+      const int lf = mf ? (int)__builtin_ctzll(mf) : 0;
+      const int f = __shfl(found, lf);
+      const double flo = __shfl(lo, lf), fhi = __shfl(hi, lf);
+      if (lane == 0) {
+        cs->j0 = mf ? f : -1;
+        cs->p_lo = flo;
+        cs->p_hi = fhi;
+      }
+    }
+    __syncthreads();
+    if (cs->j0 < 0 || !(cs->p_hi >= tau + marg) || !(cs->p_lo < tau - marg)) mode = 0;
+  }
+  if (mode == 0) {
+    __syncthreads();
+    return 0;
+  }
+  // 4. the kept prefix: keys >= klo, and at the cut key ids <= idc; compacted
+  // in no particular order
+  const uint64_t ce = mode == 2 ? cut[cs->j0] : 0ull;
+  const uint32_t klo = mode == 2 ? pk_key(ce) : kfb + 1u;
+  const uint32_t kcut = mode == 2 ? pk_key(ce) : 0u;
+  const uint32_t idc = mode == 2 ? pk_id(ce) : 0u;
+  uint64_t* da = A.dense_a + (int64_t)row * A.dense_ld;
+  __syncthreads();
+  {
+    uint32_t nx[P2];
+    cert_load<DT, PEN, P2>(rc, V, 0, nx);
+    for (int64_t base = 0; base < V; base += (int64_t)NT * P2) {
+      uint32_t kk[P2];
+#pragma unroll
+      for (int q = 0; q < P2; ++q) kk[q] = nx[q];
+      if (base + (int64_t)NT * P2 < V) cert_load<DT, PEN, P2>(rc, V, base + (int64_t)NT * P2, nx);
+#pragma unroll
+      for (int q = 0; q < P2; ++q) {
+        const uint32_t id = (uint32_t)(base + (int64_t)q * NT + tid);
+        const bool keep = kk[q] >= klo && !(kk[q] == kcut && id > idc);
+        const uint64_t km = __ballot(keep);
+        if (km) {
+          const int first = (int)__builtin_ctzll(km);
+          uint32_t s0 = 0u;
+          if (lane == first) s0 = atomicAdd(&cs->nk, (uint32_t)__popcll(km));
+          s0 = (uint32_t)__builtin_amdgcn_readlane((int)s0, first);
+          if (keep) da[s0 + lanes_below(km)] = pack(kk[q], id);
+        }
+      }
+    }
+  }
+  __syncthreads();
+  const int64_t nk = (int64_t)cs->nk;
+  const float Mf = M, invTf = (float)invT;
+  const int nd = A.mode == MODE_VERIFY ? 1 : A.n_draws;
+  for (int d = 0; d < nd; ++d) {
+    const uint64_t pk = position_key(P.seed, position_of(A, row, d));
+    // the largest binary32 score ...
+    float smax = -__builtin_inff();
+    for (int64_t j0 = 0; j0 < nk; j0 += (int64_t)NT * DRB) {
+      uint64_t ev[DRB];
+#pragma unroll
+      for (int q = 0; q < DRB; ++q) {
+        const int64_t j = j0 + (int64_t)q * NT + tid;
+        ev[q] = da[j < nk ? j : nk - 1];
+      }
+#pragma unroll
+      for (int q = 0; q < DRB; ++q) {
+        const uint64_t e = ev[q];
+        const float s = score_approx((key2f(pk_key(e)) - Mf) * invTf, pk, pk_id(e));
+        smax = (j0 + (int64_t)q * NT + tid < nk && s > smax) ? s : smax;
+      }
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+      const float t = __shfl_xor(smax, o);
+      smax = t > smax ? t : smax;
+    }
+    __syncthreads();
+    if (lane == 0) redd[wave] = (double)smax;
+    __syncthreads();
+    double sm = redd[0];
+#pragma unroll
+    for (int q = 1; q < NW; ++q) sm = redd[q] > sm ? redd[q] : sm;
+    const float thr = (float)sm - 2.0f * SC_TOL;
+    // ... then the exact z + g of the entries within 2 SC_TOL of it
+    double best = -__builtin_inf();
+    uint64_t be = 0ull;
+    for (int64_t j0 = 0; j0 < nk; j0 += (int64_t)NT * DRB) {
+      uint64_t ev[DRB];
+#pragma unroll
+      for (int q = 0; q < DRB; ++q) {
+        const int64_t j = j0 + (int64_t)q * NT + tid;
+        ev[q] = da[j < nk ? j : nk - 1];
+      }
+      uint32_t hit = 0u;
+#pragma unroll
+      for (int q = 0; q < DRB; ++q) {
+        const uint64_t e = ev[q];
+        const float s = score_approx((key2f(pk_key(e)) - Mf) * invTf, pk, pk_id(e));
+        hit |= (j0 + (int64_t)q * NT + tid < nk && s >= thr) ? (1u << q) : 0u;
+      }
+      while (hit) {  // the few entries near the largest score: exact binary64 z + g
+        const int q = __builtin_ctz(hit);
+        hit &= hit - 1u;
+        uint64_t e = ev[0];
+#pragma unroll
+        for (int r = 1; r < DRB; ++r) e = r == q ? ev[r] : e;
+        const double z = ((double)key2f(pk_key(e)) - Md) / T;
+        const double x = z + gumbel_from_key(pk, pk_id(e));
+        if (x > best || (x == best && e > be)) {
+          best = x;
+          be = e;
+        }
+      }
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+      const double ob = __shfl_xor(best, o);
+      const uint64_t oe = (uint64_t)__shfl_xor((long long)be, o);
+      if (ob > best || (ob == best && oe > be)) {
+        best = ob;
+        be = oe;
+      }
+    }
+    __syncthreads();
+    if (lane == 0) {
+      redd[wave] = best;
+      redu[wave] = be;
+    }
+    __syncthreads();
+    if (tid == 0) {
+      double b = redd[0];
+      uint64_t e = redu[0];
+      for (int q = 1; q < NW; ++q) {
+        if (redd[q] > b || (redd[q] == b && redu[q] > e)) {
+          b = redd[q];
+          e = redu[q];
+        }
+      }
+      A.out_ids[(int64_t)row * A.n_draws + d] = pk_id(e);
+    }
+  }
+  __syncthreads();
+  return (int64_t)n;
+}
+
+// ---------------------------------------------------------------------------
 // smp_row: one block of 8 wave64s per row, streaming the whole row.
 //
 // The row is read in chunks of 2,048 logits (32 values per lane, 16-byte
@@ -2367,6 +2847,7 @@ __global__ __launch_bounds__(NT) void smp_row(SmpArgs A) {
     const uint32_t theta_f = row_threshold(plan, P, M, theta);
     bool dense = fdense || (P.zcheck && plan.sampled);
     bool zfail = false;
+    bool drawn = false;  // the certified tail made the draws
     int64_t ncand = 0;
     bool sorted = false;
     // a single draw that the wave path takes: its weights and scores can be
@@ -2453,25 +2934,34 @@ __global__ __launch_bounds__(NT) void smp_row(SmpArgs A) {
       wbuf = fl.w;
     } else {
       const uint32_t trel = relevance_key(M, P.temperature);
-      ncand = dense_build<DT, PEN>(A, rc, row, trel, plan.need_rel, plan.KB, (uint32_t*)fl.cand,
-                                   (uint64_t*)fl.buf);
-      __syncthreads();
+      // a sampled version-3 row whose lists fit the waves' length: the cut
+      // certified without sorting the row when the bounds allow it
+      int64_t nc = 0;
+      if (!fdense && plan.sampled && plan.need_rel && P.version == YSKN_V3 && !P.zcheck)
+        nc = dense_certified<DT, PEN>(A, P, rc, row, M, trel, plan, fl, red_f64, red_u64);
+      drawn = nc > 0;
+      if (drawn) ncand = nc;
       cand = A.dense_a + (int64_t)row * A.dense_ld;
       wbuf = A.dense_w + (int64_t)row * A.dense_ld;
-      if (P.zcheck && plan.sampled) {
-        // The reference fails the row when any of its k candidates has a
-        // non-finite z = (l - l_0) / T (output_head_sampler.rs:146-153); z
-        // falls with l, so the k-th largest value decides.
-        uint32_t* lw = (uint32_t*)fl.cand;
-        const int64_t kk = plan.k_eff < (int64_t)V ? plan.k_eff : (int64_t)V;
-        const uint32_t kkey = radix_kth_key<DT, PEN>(rc, V, kk, lw, lw + 512 + NW * 256);
-        const double z = ((double)key2f(kkey) - (double)M) / P.temperature;
-        zfail = !(z - z == 0.0);
+      if (!drawn) {
+        ncand = dense_build<DT, PEN>(A, rc, row, trel, plan.need_rel, plan.KB, (uint32_t*)fl.cand,
+                                     (uint64_t*)fl.buf);
         __syncthreads();
+        if (P.zcheck && plan.sampled) {
+          // The reference fails the row when any of its k candidates has a
+          // non-finite z = (l - l_0) / T (output_head_sampler.rs:146-153); z
+          // falls with l, so the k-th largest value decides.
+          uint32_t* lw = (uint32_t*)fl.cand;
+          const int64_t kk = plan.k_eff < (int64_t)V ? plan.k_eff : (int64_t)V;
+          const uint32_t kkey = radix_kth_key<DT, PEN>(rc, V, kk, lw, lw + 512 + NW * 256);
+          const double z = ((double)key2f(kkey) - (double)M) / P.temperature;
+          zfail = !(z - z == 0.0);
+          __syncthreads();
+        }
+        // the first 64 sorted candidates in LDS too: every output and the
+        // one-wave tail read only those (LDS reads, not generic ones)
+        for (int i = tid; i < 64; i += NT) fl.cand[i] = i < ncand ? cand[i] : 0ull;
       }
-      // the first 64 sorted candidates in LDS too: every output and the
-      // one-wave tail read only those (LDS reads, not generic ones)
-      for (int i = tid; i < 64; i += NT) fl.cand[i] = i < ncand ? cand[i] : 0ull;
     }
 
     __syncthreads();  // the sorted candidates are visible to every thread
@@ -2569,6 +3059,8 @@ __global__ __launch_bounds__(NT) void smp_row(SmpArgs A) {
       } else if (P.greedy) {
         const int nd = A.mode == MODE_VERIFY ? 1 : A.n_draws;
         for (int d = tid; d < nd; d += NT) A.out_ids[(int64_t)row * A.n_draws + d] = amax;
+      } else if (drawn) {
+        // written by the certified tail
       } else if (ncand <= 64 && (A.mode == MODE_VERIFY || A.n_draws == 1)) {
         // one draw over at most 64 candidates: wave 0 alone
         if (wave == 0) {
@@ -2597,6 +3089,7 @@ __global__ __launch_bounds__(NT) void smp_row(SmpArgs A) {
     if (tid == 0 && A.stats) {
       atomicAdd(&A.stats[STAT_ROWS], 1ull);
       if (dense) atomicAdd(&A.stats[STAT_DENSE_ROWS], 1ull);
+      if (drawn) atomicAdd(&A.stats[STAT_CERT_ROWS], 1ull);
       atomicAdd(&A.stats[STAT_CANDIDATES], (unsigned long long)ncand);
     }
   } else if (A.out_ids) {

@@ -559,7 +559,7 @@ class DeviceSampler:
     def sync(self) -> None:
         _raise(self.L.yskn_smp_sync(self.h, self._stream()))
 
-    STAT_NAMES = ("rows", "dense_rows", "reserved", "candidates")
+    STAT_NAMES = ("rows", "dense_rows", "certified_rows", "candidates")
 
     def stats(self) -> dict:
         """Cumulative profiling counters of the handle (synchronises)."""
