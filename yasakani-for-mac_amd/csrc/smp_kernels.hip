@@ -1912,6 +1912,16 @@ __device__ __forceinline__ float score_approx(float zf, uint64_t pk, uint32_t to
   return zf - logf(l1);
 }
 
+// Entries j0 + q * NT + tid of the compacted kept set (clamped: all DRB
+// loads issued together).
+__device__ __forceinline__ void draw_load(const uint64_t* da, int64_t nk, int64_t j0, uint64_t (&v)[DRB]) {
+#pragma unroll
+  for (int q = 0; q < DRB; ++q) {
+    const int64_t j = j0 + (int64_t)q * NT + (int64_t)threadIdx.x;
+    v[q] = da[j < nk ? j : nk - 1];
+  }
+}
+
 struct CertShared {
   double R;            // sum of the bucket sums
   double a_cut;        // bucket sums before the cut bucket
@@ -1925,17 +1935,22 @@ struct CertShared {
   int32_t j0;          // cut position in the sorted cut bucket (-1: not found)
 };
 
-// Keys of elements base + q * NT + tid (0 past the row). Every load is
-// issued, at a clamped index, so that all PER are in flight together (a
-// load behind a per-element branch waits for the one before it).
+// Raw bits of elements base + q * NT + tid. Every load is issued, at a
+// clamped index, so that all PER are in flight together (a load behind a
+// per-element branch waits for the one before it); the bits are turned into
+// keys only where they are used (cert_keys), so that the loads of the next
+// tile stay in flight while a tile is processed.
 template <int DT, bool PEN, int PER>
-__device__ __forceinline__ void cert_load(const RowCtx& rc, int V, int64_t base, uint32_t (&k)[PER]) {
-  uint32_t b[PER];
+__device__ __forceinline__ void cert_load(const RowCtx& rc, int V, int64_t base, uint32_t (&b)[PER]) {
 #pragma unroll
   for (int q = 0; q < PER; ++q) {
     const int64_t i = base + (int64_t)q * NT + (int64_t)threadIdx.x;
     b[q] = value_bits<DT, PEN>(rc, i < V ? i : (int64_t)V - 1);
   }
+}
+// Keys of those elements (0 past the row).
+template <int PER>
+__device__ __forceinline__ void cert_keys(int V, int64_t base, const uint32_t (&b)[PER], uint32_t (&k)[PER]) {
 #pragma unroll
   for (int q = 0; q < PER; ++q) {
     const int64_t i = base + (int64_t)q * NT + (int64_t)threadIdx.x;
@@ -1977,8 +1992,7 @@ __device__ __forceinline__ int64_t dense_certified(const SmpArgs& A, const DevPa
     cert_load<DT, PEN, P1>(rc, V, 0, nx);
     for (int64_t base = 0; base < V; base += (int64_t)NT * P1) {
       uint32_t kk[P1];
-#pragma unroll
-      for (int q = 0; q < P1; ++q) kk[q] = nx[q];
+      cert_keys<P1>(V, base, nx, kk);
       if (base + (int64_t)NT * P1 < V) cert_load<DT, PEN, P1>(rc, V, base + (int64_t)NT * P1, nx);
 #pragma unroll
       for (int q = 0; q < P1; ++q) {
@@ -2074,8 +2088,7 @@ __device__ __forceinline__ int64_t dense_certified(const SmpArgs& A, const DevPa
     cert_load<DT, PEN, P2>(rc, V, 0, nx);
     for (int64_t base = 0; base < V; base += (int64_t)NT * P2) {
       uint32_t kk[P2];
-#pragma unroll
-      for (int q = 0; q < P2; ++q) kk[q] = nx[q];
+      cert_keys<P2>(V, base, nx, kk);
       if (base + (int64_t)NT * P2 < V) cert_load<DT, PEN, P2>(rc, V, base + (int64_t)NT * P2, nx);
 #pragma unroll
       for (int q = 0; q < P2; ++q) {
@@ -2175,8 +2188,7 @@ __device__ __forceinline__ int64_t dense_certified(const SmpArgs& A, const DevPa
     cert_load<DT, PEN, P2>(rc, V, 0, nx);
     for (int64_t base = 0; base < V; base += (int64_t)NT * P2) {
       uint32_t kk[P2];
-#pragma unroll
-      for (int q = 0; q < P2; ++q) kk[q] = nx[q];
+      cert_keys<P2>(V, base, nx, kk);
       if (base + (int64_t)NT * P2 < V) cert_load<DT, PEN, P2>(rc, V, base + (int64_t)NT * P2, nx);
 #pragma unroll
       for (int q = 0; q < P2; ++q) {
@@ -2201,13 +2213,13 @@ __device__ __forceinline__ int64_t dense_certified(const SmpArgs& A, const DevPa
     const uint64_t pk = position_key(P.seed, position_of(A, row, d));
     // the largest binary32 score ...
     float smax = -__builtin_inff();
+    uint64_t nv[DRB];  // the next round's entries, in flight while a round is scored
+    if (nk > 0) draw_load(da, nk, 0, nv);
     for (int64_t j0 = 0; j0 < nk; j0 += (int64_t)NT * DRB) {
       uint64_t ev[DRB];
 #pragma unroll
-      for (int q = 0; q < DRB; ++q) {
-        const int64_t j = j0 + (int64_t)q * NT + tid;
-        ev[q] = da[j < nk ? j : nk - 1];
-      }
+      for (int q = 0; q < DRB; ++q) ev[q] = nv[q];
+      if (j0 + (int64_t)NT * DRB < nk) draw_load(da, nk, j0 + (int64_t)NT * DRB, nv);
 #pragma unroll
       for (int q = 0; q < DRB; ++q) {
         const uint64_t e = ev[q];
@@ -2230,13 +2242,12 @@ __device__ __forceinline__ int64_t dense_certified(const SmpArgs& A, const DevPa
     // ... then the exact z + g of the entries within 2 SC_TOL of it
     double best = -__builtin_inf();
     uint64_t be = 0ull;
+    if (nk > 0) draw_load(da, nk, 0, nv);
     for (int64_t j0 = 0; j0 < nk; j0 += (int64_t)NT * DRB) {
       uint64_t ev[DRB];
 #pragma unroll
-      for (int q = 0; q < DRB; ++q) {
-        const int64_t j = j0 + (int64_t)q * NT + tid;
-        ev[q] = da[j < nk ? j : nk - 1];
-      }
+      for (int q = 0; q < DRB; ++q) ev[q] = nv[q];
+      if (j0 + (int64_t)NT * DRB < nk) draw_load(da, nk, j0 + (int64_t)NT * DRB, nv);
       uint32_t hit = 0u;
 #pragma unroll
       for (int q = 0; q < DRB; ++q) {
@@ -2301,7 +2312,7 @@ __device__ __forceinline__ int64_t dense_certified(const SmpArgs& A, const DevPa
 // the reference's truncation and draw: no second launch, no traffic between
 // blocks.
 // ---------------------------------------------------------------------------
-template <int DT, bool VEC, bool PEN>
+template <int DT, bool VEC, bool PEN, bool CERT>
 __global__ __launch_bounds__(NT) void smp_row(SmpArgs A) {
   __shared__ RowLds fl;
   __shared__ RowShared sh;
@@ -2937,8 +2948,10 @@ __global__ __launch_bounds__(NT) void smp_row(SmpArgs A) {
       // a sampled version-3 row whose lists fit the waves' length: the cut
       // certified without sorting the row when the bounds allow it
       int64_t nc = 0;
-      if (!fdense && plan.sampled && plan.need_rel && P.version == YSKN_V3 && !P.zcheck)
-        nc = dense_certified<DT, PEN>(A, P, rc, row, M, trel, plan, fl, red_f64, red_u64);
+      if constexpr (CERT) {
+        if (!fdense && plan.sampled && plan.need_rel && P.version == YSKN_V3 && !P.zcheck)
+          nc = dense_certified<DT, PEN>(A, P, rc, row, M, trel, plan, fl, red_f64, red_u64);
+      }
       drawn = nc > 0;
       if (drawn) ncand = nc;
       cand = A.dense_a + (int64_t)row * A.dense_ld;
@@ -3280,9 +3293,18 @@ __global__ __launch_bounds__(PP_NT) void smp_penalty_prep(PenArgs A) {
 }
 
 // ---------------------------------------------------------------------------
+// Launches of fewer than CERT_ROWS rows (the segmented ones) carry the
+// certified dense tail; a dense row of a larger launch, where one block
+// streams each row and such rows are rare, takes the sorting path, which
+// keeps that kernel's code as small as it was without the tail.
+constexpr int CERT_ROWS = 192;
+
 template <int DT, bool VEC, bool PEN>
 static hipError_t launch_t(const SmpArgs& a, hipStream_t st) {
-  hipLaunchKernelGGL((smp_row<DT, VEC, PEN>), dim3((unsigned)(a.rows * a.nseg)), dim3(NT), 0, st, a);
+  if (a.rows < CERT_ROWS)
+    hipLaunchKernelGGL((smp_row<DT, VEC, PEN, true>), dim3((unsigned)(a.rows * a.nseg)), dim3(NT), 0, st, a);
+  else
+    hipLaunchKernelGGL((smp_row<DT, VEC, PEN, false>), dim3((unsigned)(a.rows * a.nseg)), dim3(NT), 0, st, a);
   return hipGetLastError();
 }
 
