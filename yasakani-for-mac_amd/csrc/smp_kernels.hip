@@ -1845,14 +1845,15 @@ __device__ __forceinline__ uint32_t compact_entries(const uint64_t* src, uint32_
 //     only when no weight lies within 2^-40 of min-p (relative); otherwise,
 //     or when a collection does not fit, the function returns 0 and the
 //     caller sorts the row (the exact path);
-//  4. the kept candidates are a prefix of the order: every element with key
-//     above the cut key and, at the cut key, the ids up to the cut id. They
-//     are compacted; a draw takes the largest binary32 score (within
-//     SC_TOL of z + g, score_approx) over them, then the exact binary64
-//     z + g of the entries within 2 SC_TOL of it, ties to the earlier
-//     candidate (the reference's strict > in candidate order).
+//  4. the kept candidates are a prefix of the order: the second pass writes
+//     out those before the cut bucket, the sorted cut bucket adds its part.
+//     A draw takes the largest binary32 score (within SC_TOL of z + g,
+//     score_approx) over them, then the exact binary64 z + g of the entries
+//     within 2 SC_TOL of it, ties to the earlier candidate (the reference's
+//     strict > in candidate order).
 // Passes over the row keep the next tile's loads in flight while a tile is
-// processed. On success fl.cand holds the first KB candidates, sorted,
+// processed. The total is also summed in a second order; a difference
+// beyond the bound fails the certification too. On success fl.cand holds the first KB candidates, sorted,
 // out_ids the draws, and the return value is the number of relevant
 // elements. Block-wide.
 // ---------------------------------------------------------------------------
@@ -1987,6 +1988,7 @@ __device__ __forceinline__ int64_t dense_certified(const SmpArgs& A, const DevPa
   const double mp_lo = P.min_p * (1.0 - 0x1p-40), mp_hi = P.min_p * (1.0 + 0x1p-40);
   uint32_t kfb = 0u;
   bool amb = false;  // a weight too close to min-p to decide
+  double wrel = 0.0;
   {
     uint32_t nx[P1];
     cert_load<DT, PEN, P1>(rc, V, 0, nx);
@@ -1994,22 +1996,31 @@ __device__ __forceinline__ int64_t dense_certified(const SmpArgs& A, const DevPa
       uint32_t kk[P1];
       cert_keys<P1>(V, base, nx, kk);
       if (base + (int64_t)NT * P1 < V) cert_load<DT, PEN, P1>(rc, V, base + (int64_t)NT * P1, nx);
+      // every element's weight and bucket first, outside the branches, so
+      // that the elements' dependent chains interleave
+      double wv[P1];
+      uint32_t bv[P1];
 #pragma unroll
       for (int q = 0; q < P1; ++q) {
         const double z = ((double)key2f(kk[q]) - Md) * invT;
-        const double w = exp_approx(z);
+        wv[q] = exp_approx(z);
+        bv[q] = cert_bucket(z);
+        wrel += kk[q] >= trel ? wv[q] : 0.0;
+      }
+#pragma unroll
+      for (int q = 0; q < P1; ++q) {
         if (kk[q] >= trel) {
-          const uint32_t b = cert_bucket(z);
-          atomicAdd(&hw[b], w);
-          atomicAdd(&hc[b], 1u);
-          if (w < mp_lo && kk[q] > kfb) kfb = kk[q];
-          amb |= w >= mp_lo && w <= mp_hi;
+          atomicAdd(&hw[bv[q]], wv[q]);
+          atomicAdd(&hc[bv[q]], 1u);
+          if (wv[q] < mp_lo && kk[q] > kfb) kfb = kk[q];
+          amb |= wv[q] >= mp_lo && wv[q] <= mp_hi;
         }
       }
     }
   }
   kfb = (uint32_t)block_max_u64((uint64_t)kfb, redu);
   amb = block_max_u64(amb ? 1ull : 0ull, redu) != 0ull;
+  wrel = block_sum_f64(wrel, redd);  // the total once more, in another order (a cross-check)
   const uint32_t bfb = kfb ? cert_bucket(((double)key2f(kfb) - Md) * invT) : (uint32_t)CB_NB;
   __syncthreads();
   // the running sums over the buckets (wave 0; lane l owns buckets 64l..64l+63)
@@ -2081,7 +2092,12 @@ __device__ __forceinline__ int64_t dense_certified(const SmpArgs& A, const DevPa
     __syncthreads();
     return 0;
   }
-  // 2. collect the cut bucket and the head; sum what min-p keeps of its bucket
+  // 2. collect the cut bucket and the head; sum what min-p keeps of its
+  // bucket; write out the entries kept whichever cut holds (every kept entry
+  // outside the cut bucket: with the min-p cut, S_(m-1) < top_p * total - E
+  // puts every kept entry at or before the cut bucket; with the top-p cut,
+  // every entry before the cut bucket precedes the cut and so lies above kfb)
+  uint64_t* da = A.dense_a + (int64_t)row * A.dense_ld;
   double pfb = 0.0;
   {
     uint32_t nx[P2];
@@ -2092,10 +2108,20 @@ __device__ __forceinline__ int64_t dense_certified(const SmpArgs& A, const DevPa
       if (base + (int64_t)NT * P2 < V) cert_load<DT, PEN, P2>(rc, V, base + (int64_t)NT * P2, nx);
 #pragma unroll
       for (int q = 0; q < P2; ++q) {
+        const double z = ((double)key2f(kk[q]) - Md) * invT;
+        const uint32_t b = cert_bucket(z);
+        const uint64_t e = pack(kk[q], (uint32_t)(base + (int64_t)q * NT + tid));
+        // kept whichever cut holds: before the cut bucket and above kfb
+        const bool wr = kk[q] >= trel && b < bcut && kk[q] > kfb;
+        const uint64_t wm = __ballot(wr);
+        if (wm) {
+          const int first = (int)__builtin_ctzll(wm);
+          uint32_t s0 = 0u;
+          if (lane == first) s0 = atomicAdd(&cs->nk, (uint32_t)__popcll(wm));
+          s0 = (uint32_t)__builtin_amdgcn_readlane((int)s0, first);
+          if (wr) da[s0 + lanes_below(wm)] = e;
+        }
         if (kk[q] >= trel) {
-          const double z = ((double)key2f(kk[q]) - Md) * invT;
-          const uint32_t b = cert_bucket(z);
-          const uint64_t e = pack(kk[q], (uint32_t)(base + (int64_t)q * NT + tid));
           if (b == bfb && kk[q] > kfb) pfb += exp_approx(z);
           if (b == bcut) {
             const uint32_t s = atomicAdd(&cs->ncut, 1u);
@@ -2171,38 +2197,18 @@ __device__ __forceinline__ int64_t dense_certified(const SmpArgs& A, const DevPa
     __syncthreads();
     if (cs->j0 < 0 || !(cs->p_hi >= tau + marg) || !(cs->p_lo < tau - marg)) mode = 0;
   }
+  if (!(fabs(wrel - R) <= marg)) mode = 0;  // the two sums disagree beyond their bounds
   if (mode == 0) {
     __syncthreads();
     return 0;
   }
-  // 4. the kept prefix: keys >= klo, and at the cut key ids <= idc; compacted
-  // in no particular order
-  const uint64_t ce = mode == 2 ? cut[cs->j0] : 0ull;
-  const uint32_t klo = mode == 2 ? pk_key(ce) : kfb + 1u;
-  const uint32_t kcut = mode == 2 ? pk_key(ce) : 0u;
-  const uint32_t idc = mode == 2 ? pk_id(ce) : 0u;
-  uint64_t* da = A.dense_a + (int64_t)row * A.dense_ld;
-  __syncthreads();
+  // 4. the kept entries of the cut bucket join those written in pass 2:
+  // with the top-p cut its first j0 + 1, with the min-p cut those above kfb
   {
-    uint32_t nx[P2];
-    cert_load<DT, PEN, P2>(rc, V, 0, nx);
-    for (int64_t base = 0; base < V; base += (int64_t)NT * P2) {
-      uint32_t kk[P2];
-      cert_keys<P2>(V, base, nx, kk);
-      if (base + (int64_t)NT * P2 < V) cert_load<DT, PEN, P2>(rc, V, base + (int64_t)NT * P2, nx);
-#pragma unroll
-      for (int q = 0; q < P2; ++q) {
-        const uint32_t id = (uint32_t)(base + (int64_t)q * NT + tid);
-        const bool keep = kk[q] >= klo && !(kk[q] == kcut && id > idc);
-        const uint64_t km = __ballot(keep);
-        if (km) {
-          const int first = (int)__builtin_ctzll(km);
-          uint32_t s0 = 0u;
-          if (lane == first) s0 = atomicAdd(&cs->nk, (uint32_t)__popcll(km));
-          s0 = (uint32_t)__builtin_amdgcn_readlane((int)s0, first);
-          if (keep) da[s0 + lanes_below(km)] = pack(kk[q], id);
-        }
-      }
+    const int32_t j0 = mode == 2 ? cs->j0 : -1;
+    for (uint32_t j = (uint32_t)tid; j < ncut; j += NT) {
+      const uint64_t e = cut[j];
+      if (mode == 2 ? (int32_t)j <= j0 : pk_key(e) > kfb) da[atomicAdd(&cs->nk, 1u)] = e;
     }
   }
   __syncthreads();
