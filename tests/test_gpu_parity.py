@@ -450,6 +450,69 @@ def test_certified_dense_tail_with_penalties_and_coarse_values():
     d.close()
 
 
+@pytest.mark.parametrize("seed", [1, 2, 3])
+def test_certified_dense_tail_randomised(seed):
+    """Many dense rows with random shapes and parameters (scale, temperature,
+    top-p including 1, min-p including 0, version 2 rows that take the
+    sorting path, heavy tails, repeated values): every id is the oracle's,
+    and most rows are served by the certified tail."""
+    rng = np.random.default_rng(1000 + seed)
+    rows, V = 40, 30_000
+    x = np.empty((rows, V), np.float32)
+    for r in range(rows):
+        kind = r % 4
+        sc = rng.uniform(0.3, 4.0)
+        if kind == 0:
+            x[r] = sc * rng.standard_normal(V)
+        elif kind == 1:
+            x[r] = sc * rng.standard_t(3, V)
+        elif kind == 2:
+            x[r] = np.round(sc * rng.standard_normal(V) * 64) / 64  # repeated values
+        else:
+            x[r] = sc * rng.uniform(-1, 1, V)
+    sps = [SamplingParameters(temperature_milli=int(rng.integers(200, 3000)),
+                              top_p_milli=int(rng.choice([500, 800, 900, 950, 990, 999, 1000])),
+                              min_p_milli=int(rng.choice([0, 0, 1, 5, 50, 200])), top_k=0,
+                              seed=int(rng.integers(0, 2**62)),
+                              version=INVERSE_CUMULATIVE if r % 10 == 9 else GUMBEL) for r in range(rows)]
+    d = DeviceSampler(rows, V, extended_top_k=True)
+    d.set_params(sps)
+    pos = rng.integers(0, 2**40, rows)
+    out = _run(d, torch.from_numpy(x).to(DEV), pos, argmax=True, top8=True)
+    ref = pmap(lambda r: oracle_select(x[r], int(pos[r]), sps[r], extension=True), range(rows))
+    got = to_u32(out["ids"]).reshape(-1)
+    bad = [r for r in range(rows) if got[r] != ref[r]]
+    assert not bad, [(r, int(got[r]), ref[r], sps[r]) for r in bad]
+    for r in range(rows):
+        assert list(to_u32(out["top8_ids"])[r]) == list(O.top_tokens(x[r], 8)), r
+    st = d.stats()
+    print("path counters", st, flush=True)
+    assert st["certified_rows"] >= rows // 2
+    d.close()
+
+
+def test_certified_dense_tail_in_verify():
+    """Verify rows with top-k disabled: the certified tail draws the target
+    row's token, the accept rule sees the oracle's."""
+    rng = np.random.default_rng(77)
+    M, V = 6, 40_000
+    tgt = (1.5 * rng.standard_normal((M, V))).astype(np.float32)
+    sp = SamplingParameters(temperature_milli=900, top_p_milli=930, min_p_milli=0, top_k=0, seed=0xC0FFEE)
+    base = 5_000
+    drafts = [oracle_select(tgt[j], base + j + 1, sp, extension=True) for j in range(M - 1)]
+    d = DeviceSampler(M, V, extended_top_k=True)
+    d.set_params(sp)
+    ids, res, _keep = d.verify(torch.from_numpy(tgt).to(DEV), torch.tensor(drafts, device=DEV),
+                               torch.tensor([base], device=DEV))
+    d.sync()
+    sel, em, acc, stop = O.verify(tgt, drafts, base, oracle_params(sp, True))
+    r = res.cpu().numpy().astype(np.int64)
+    assert (r[0], r[1], r[2]) == (acc, em, sel[-1])
+    assert list(to_u32(ids)[:em]) == list(sel)
+    assert d.stats()["certified_rows"] > 0
+    d.close()
+
+
 # ---------------------------------------------------------------------------
 # the five workloads at full size
 # ---------------------------------------------------------------------------
