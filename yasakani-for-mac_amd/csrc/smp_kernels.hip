@@ -2315,7 +2315,9 @@ __device__ __forceinline__ int64_t dense_certified(const SmpArgs& A, const DevPa
 // the bounds as they stand and appends the elements that can matter to an
 // LDS buffer. After the stream the same block sorts the candidates and runs
 // the reference's truncation and draw: no second launch, no traffic between
-// blocks.
+// blocks. CERT: the form of the smaller launches, whose rows may be split
+// into segments (one block each, the last one finishing the row) and whose
+// dense rows try the certified tail; without it, one block per row.
 // ---------------------------------------------------------------------------
 template <int DT, bool VEC, bool PEN, bool CERT>
 __global__ __launch_bounds__(NT) void smp_row(SmpArgs A) {
@@ -2338,7 +2340,7 @@ __global__ __launch_bounds__(NT) void smp_row(SmpArgs A) {
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   // A row is split into nseg segments of whole chunks, one block each; with
   // nseg = 1 the block streams the whole row and finishes it directly.
-  const int nseg = A.nseg;
+  const int nseg = CERT ? A.nseg : 1;  // the large-launch form streams one row per block
   const int row = (int)blockIdx.x / nseg;
   const int seg = (int)blockIdx.x - row * nseg;
   const int32_t V = A.V;
@@ -3298,15 +3300,16 @@ __global__ __launch_bounds__(PP_NT) void smp_penalty_prep(PenArgs A) {
 }
 
 // ---------------------------------------------------------------------------
-// Launches of fewer than CERT_ROWS rows (the segmented ones) carry the
-// certified dense tail; a dense row of a larger launch, where one block
-// streams each row and such rows are rare, takes the sorting path, which
-// keeps that kernel's code as small as it was without the tail.
+// Launches of fewer than CERT_ROWS rows, and every segmented launch, use the
+// form with the row segments and the certified dense tail. Larger launches
+// stream one row per block (no segment code) and a dense row there, rare,
+// takes the sorting path: that kernel keeps the code of the stream and the
+// common finish alone.
 constexpr int CERT_ROWS = 192;
 
 template <int DT, bool VEC, bool PEN>
 static hipError_t launch_t(const SmpArgs& a, hipStream_t st) {
-  if (a.rows < CERT_ROWS)
+  if (a.rows < CERT_ROWS || a.nseg > 1)
     hipLaunchKernelGGL((smp_row<DT, VEC, PEN, true>), dim3((unsigned)(a.rows * a.nseg)), dim3(NT), 0, st, a);
   else
     hipLaunchKernelGGL((smp_row<DT, VEC, PEN, false>), dim3((unsigned)(a.rows * a.nseg)), dim3(NT), 0, st, a);
