@@ -2320,7 +2320,23 @@ __device__ __forceinline__ int64_t dense_certified(const SmpArgs& A, const DevPa
 // dense rows try the certified tail; without it, one block per row.
 // ---------------------------------------------------------------------------
 template <int DT, bool VEC, bool PEN, bool CERT>
-__global__ __launch_bounds__(NT) void smp_row(SmpArgs A) {
+__global__ __launch_bounds__(NT) void smp_row(SmpArgs Ain) {
+  // The large-launch form serves one feature set: sampling at explicit
+  // positions, one draw per row, lists of at most KBMAX entries, no
+  // advance, no NLL targets, nothing forced (the host sends every other
+  // launch to the general form). Pinning those fields leaves the rest out
+  // of that kernel's code.
+  SmpArgs A = Ain;
+  if constexpr (!CERT) {
+    A.nseg = 1;
+    A.mode = MODE_SAMPLE;
+    A.n_draws = 1;
+    A.pos_mode = POS_ARRAY;
+    A.adv_pos = nullptr;
+    A.adv_tok = nullptr;
+    A.nll_targets = nullptr;
+    A.force_dense = 0;
+  }
   __shared__ RowLds fl;
   __shared__ RowShared sh;
   __shared__ uint64_t red_u64[NW];
@@ -2340,7 +2356,7 @@ __global__ __launch_bounds__(NT) void smp_row(SmpArgs A) {
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   // A row is split into nseg segments of whole chunks, one block each; with
   // nseg = 1 the block streams the whole row and finishes it directly.
-  const int nseg = CERT ? A.nseg : 1;  // the large-launch form streams one row per block
+  const int nseg = A.nseg;
   const int row = (int)blockIdx.x / nseg;
   const int seg = (int)blockIdx.x - row * nseg;
   const int32_t V = A.V;
@@ -2370,7 +2386,7 @@ __global__ __launch_bounds__(NT) void smp_row(SmpArgs A) {
   const RowPlan plan = make_plan(A, P);
   // the exact dense path from the start: forced, or a prefix longer than the
   // waves' lists (top-N or logprob counts above KBMAX)
-  const bool fdense = A.force_dense != 0 || plan.KB > KBMAX;
+  const bool fdense = CERT && (A.force_dense != 0 || plan.KB > KBMAX);  // (the large form: KB <= KBMAX)
   uint32_t wflags = 0;
   const RowCtx rc = make_rowctx<PEN>(A, P, row, ES, &wflags);
   if (tid == 0) {
@@ -2997,7 +3013,7 @@ __global__ __launch_bounds__(NT) void smp_row(SmpArgs A) {
     // log of the mass (wave 1 alone, off the draw's path): one term per
     // wave, in lanes 0..NW-1
     // (more than 64 outputs: every wave writes them, and needs logZ)
-    const bool big_out = A.topn > 64 || A.n_lp > 64;
+    const bool big_out = CERT && (A.topn > 64 || A.n_lp > 64);
     double logZ = 0.0;
     if (A.want_mass && (wave == 1 || big_out)) {
       double t = 0.0;
@@ -3022,7 +3038,7 @@ __global__ __launch_bounds__(NT) void smp_row(SmpArgs A) {
       A.top20_ids[(int64_t)row * 20 + i] = in ? pk_id(fl.cand[i]) : 0xffffffffu;
       A.top20_vals[(int64_t)row * 20 + i] = in ? raw_value(fl.cand[i]) : -__builtin_inff();
     }
-    if (A.topn_ids && A.topn > 64) {
+    if (CERT && A.topn_ids && A.topn > 64) {
       for (int64_t i = tid; i < A.topn; i += NT) {
         const bool in = i < ncand;
         A.topn_ids[(int64_t)row * A.topn + i] = in ? pk_id(cand[i]) : 0xffffffffu;
@@ -3034,7 +3050,7 @@ __global__ __launch_bounds__(NT) void smp_row(SmpArgs A) {
       A.topn_ids[(int64_t)row * A.topn + i] = in ? pk_id(fl.cand[i]) : 0xffffffffu;
       if (A.topn_vals) A.topn_vals[(int64_t)row * A.topn + i] = in ? raw_value(fl.cand[i]) : -__builtin_inff();
     }
-    if (A.n_lp > 64) {
+    if (CERT && A.n_lp > 64) {
       for (int64_t i = tid; i < A.n_lp; i += NT) {
         const bool in = i < ncand;
         double lp = -__builtin_inf();
@@ -3300,16 +3316,22 @@ __global__ __launch_bounds__(PP_NT) void smp_penalty_prep(PenArgs A) {
 }
 
 // ---------------------------------------------------------------------------
-// Launches of fewer than CERT_ROWS rows, and every segmented launch, use the
-// form with the row segments and the certified dense tail. Larger launches
-// stream one row per block (no segment code) and a dense row there, rare,
-// takes the sorting path: that kernel keeps the code of the stream and the
+// Launches of fewer than CERT_ROWS rows, every segmented launch and every
+// launch that uses a feature beyond plain sampling (verify, device
+// positions, several draws, advance, NLL targets, lists longer than KBMAX,
+// the forced dense path) use the general form: row segments, the certified
+// dense tail, everything. The other large launches stream one row per block
+// with the large form, which leaves all that out (a dense row there, rare,
+// takes the sorting path): that kernel keeps the code of the stream and the
 // common finish alone.
 constexpr int CERT_ROWS = 192;
 
 template <int DT, bool VEC, bool PEN>
 static hipError_t launch_t(const SmpArgs& a, hipStream_t st) {
-  if (a.rows < CERT_ROWS || a.nseg > 1)
+  const bool large = a.rows >= CERT_ROWS && a.nseg == 1 && a.mode == MODE_SAMPLE && a.pos_mode == POS_ARRAY &&
+                     a.n_draws == 1 && a.adv_pos == nullptr && a.adv_tok == nullptr && a.nll_targets == nullptr &&
+                     a.topn <= KBMAX && a.n_lp <= KBMAX && a.force_dense == 0;
+  if (!large)
     hipLaunchKernelGGL((smp_row<DT, VEC, PEN, true>), dim3((unsigned)(a.rows * a.nseg)), dim3(NT), 0, st, a);
   else
     hipLaunchKernelGGL((smp_row<DT, VEC, PEN, false>), dim3((unsigned)(a.rows * a.nseg)), dim3(NT), 0, st, a);
