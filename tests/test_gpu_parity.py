@@ -513,6 +513,51 @@ def test_certified_dense_tail_in_verify():
     d.close()
 
 
+def test_large_launches_with_other_features():
+    """Launches of 192 rows or more that go beyond plain sampling (several
+    draws, logprob lists longer than 64, device positions, NLL, top lists)
+    run the general kernel form; plain ones the large form. Both match the
+    oracle."""
+    rng = np.random.default_rng(55)
+    rows, V = 200, 6_000
+    x = (2.0 * rng.standard_normal((rows, V))).astype(np.float32)
+    xt = torch.from_numpy(x).to(DEV)
+    sp = SamplingParameters(temperature_milli=900, top_p_milli=950, top_k=0, seed=123)
+    d = DeviceSampler(rows, V, extended_top_k=True)
+    d.set_params(sp)
+    # plain sampling with top-20 and 20 logprobs (the large form)
+    pos = np.arange(rows) + 7
+    out = _run(d, xt, pos, top20=True, n_logprobs=20)
+    assert list(to_u32(out["ids"]).reshape(-1)) == pmap(
+        lambda r: oracle_select(x[r], int(pos[r]), sp, extension=True), range(rows))
+    # several draws per row
+    pos3 = (np.arange(rows * 3).reshape(rows, 3) * 11 + 5).astype(np.int64)
+    out = _run(d, xt, pos3)
+    got = to_u32(out["ids"]).reshape(rows, 3)
+    for r in range(0, rows, 17):
+        assert list(got[r]) == list(O.sample_positions(x[r], pos3[r].astype(np.uint64), oracle_params(sp, True)))
+    # 100 logprobs per row (lists past 64)
+    out = _run(d, xt, pos, n_logprobs=100)
+    for r in range(0, rows, 23):
+        ids, lps = O.top_logprobs(x[r], 100)
+        assert list(to_u32(out["logprob_ids"])[r]) == list(ids)
+        assert_logprobs_close(out["logprobs"][r].cpu().numpy(), lps)
+    assert list(to_u32(out["ids"]).reshape(-1))[:5] == [oracle_select(x[r], int(pos[r]), sp, extension=True)
+                                                        for r in range(5)]
+    # device positions: *base + row + 1
+    base = torch.tensor([1000], dtype=torch.int64, device=DEV)
+    out = d.sample_at(xt, base)
+    d.sync()
+    assert list(to_u32(out["ids"]).reshape(-1))[:40] == [oracle_select(x[r], 1000 + r + 1, sp, extension=True)
+                                                         for r in range(40)]
+    # NLL over the same launch shape
+    tg = rng.integers(0, V, rows)
+    nll = d.nll(xt, torch.from_numpy(tg).to(DEV))
+    d.sync()
+    assert_logprobs_close(nll.cpu().numpy(), [O.nll(x[r], int(tg[r])) for r in range(rows)])
+    d.close()
+
+
 # ---------------------------------------------------------------------------
 # the five workloads at full size
 # ---------------------------------------------------------------------------
