@@ -384,6 +384,11 @@ int yskn_smp_validate_params_f64(const yskn_smp_params_f64* params, int32_t voca
  *                  (output_head_sampler.rs:221-228)
  *   fn 13: version-2 uniform (seed, position) u64 pairs -> binary64 (:196-197)
  *   fn 14: mix64   u64 -> u64 (:214-219)
+ *   fn 15: the certified dense tail's polynomial exp, binary64 -> binary64
+ *          (no counterpart in the reference: bounded, not bit-exact)
+ *   fn 16: the same tail's binary32 version-3 score from (z binary32 bits,
+ *          position key mix64(mix64(seed) ^ position), token) u64 triples ->
+ *          binary32 bits (no counterpart in the reference: bounded)
  *   fn 8:  serial binary64 prefix sums S_j = (..(w_0 + w_1) + ..) + w_j of n
  *          weights (w_0 = 1 >= w_j >= 0), as the tail computes them in
  *          parallel (output_head_sampler.rs:157-175)

@@ -113,6 +113,46 @@ def test_device_hashes_and_uniforms_match_the_oracle():
     assert all(O.mix64(int(seeds[i])) == int(m[i]) for i in sel)
 
 
+def _mix64(x):
+    x = x + np.uint64(0x9E3779B97F4A7C15)
+    x = (x ^ (x >> np.uint64(30))) * np.uint64(0xBF58476D1CE4E5B9)
+    x = (x ^ (x >> np.uint64(27))) * np.uint64(0x94D049BB133111EB)
+    return x ^ (x >> np.uint64(31))
+
+
+def test_certified_tail_approximations_stay_within_their_bounds():
+    """The certified dense tail rests on two bounded approximations, taken
+    here from the device: its polynomial exp (within 2^-46 relative of e^z
+    for z <= 0, against long double) and its binary32 version-3 score (within
+    1e-4 of the binary64 z + g, z = (l - M) / T formed as the tail forms it,
+    g the device Gumbel noise that matches the oracle bit for bit)."""
+    rng = np.random.default_rng(8)
+    z = np.concatenate([-40.0 * rng.random(300_000), -700.0 * rng.random(1000),
+                        [0.0, -0.0, -1e-300, -37.5, -40.0, -0.34657359, -0.34657360, -700.0]])
+    got = yskn_smp.pm_test(15, z.astype(np.float64)).view(np.float64)
+    ref = np.exp(z.astype(np.longdouble))
+    rel = np.abs((got.astype(np.longdouble) - ref) / ref)
+    assert float(rel.max()) <= 2.0 ** -46, float(rel.max())
+    n = 400_000
+    seeds = rng.integers(0, 2**64, n, dtype=np.uint64)
+    pos = rng.integers(0, 2**64, n, dtype=np.uint64)
+    tok = rng.integers(0, 2**32, n, dtype=np.uint64)
+    T = rng.uniform(0.2, 3.0, n)
+    l = (8.0 * rng.standard_normal(n)).astype(np.float32)
+    M = (l.astype(np.float64) + 37.5 * T * rng.random(n)).astype(np.float32)
+    M = np.maximum(M, l)
+    zf = (l - M) * (1.0 / T).astype(np.float32)  # binary32, as the tail forms it
+    pk = _mix64(_mix64(seeds) ^ pos)
+    s32 = yskn_smp.pm_test(16, np.stack([zf.view(np.uint32).astype(np.uint64), pk, tok], 1))
+    s32 = s32.astype(np.uint32).view(np.float32).astype(np.float64)
+    g = yskn_smp.pm_test(12, np.stack([seeds, pos, tok], 1)).view(np.float64)
+    exact = (l.astype(np.float64) - M.astype(np.float64)) / T + g
+    fin = np.isfinite(exact)
+    err = np.abs(s32[fin] - exact[fin])
+    assert float(err.max()) <= 1e-4, float(err.max())
+    assert np.all(np.isposinf(s32[~fin]))
+
+
 @pytest.mark.parametrize("fn", [6, 7])
 def test_device_sqrt_rn_and_rsqrt_are_correctly_rounded(fn):
     for base, n in [(0, 1 << 22), (0x3F000000, 1 << 24), (0x7F000000, 0x7F800000 - 0x7F000000)]:

@@ -4,8 +4,9 @@
 // given in host memory, so that its binary64/binary32 results can be compared
 // bit for bit with the CPU restatement. It is the counterpart of the
 // reference's yskn_pm_test (src/pm_test.cu:30-52; fn 10 = exp_d, fn 11 =
-// log_d there as here), and the tail's exact prefix-sum scan (fn 8). Not on
-// the sampling path: it allocates, copies and synchronises.
+// log_d there as here), the tail's exact prefix-sum scan (fn 8) and the two
+// bounded approximations of the certified dense tail (fn 15, 16). Not on the
+// sampling path: it allocates, copies and synchronises.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -33,6 +34,11 @@ __global__ __launch_bounds__(256) void pm_test_kernel(int fn, uint64_t base, con
     }
     case 13: o64[i] = pm_bits(uniform_v2(in[2 * i], in[2 * i + 1])); break;
     case 14: o64[i] = mix64(in[i]); break;
+    case 15: o64[i] = pm_bits(exp_approx(__longlong_as_double((long long)in[i]))); break;
+    case 16:
+      o64[i] = __float_as_uint(score_approx(__uint_as_float((uint32_t)in[3 * i]), in[3 * i + 1],
+                                            (uint32_t)in[3 * i + 2]));
+      break;
     case 6:
     case 7: {
       const uint32_t b = (uint32_t)(base + (uint64_t)i);
@@ -46,8 +52,8 @@ __global__ __launch_bounds__(256) void pm_test_kernel(int fn, uint64_t base, con
 
 int words_in(int fn) {
   switch (fn) {
-    case 10: case 11: case 14: return 1;
-    case 12: return 3;
+    case 10: case 11: case 14: case 15: return 1;
+    case 12: case 16: return 3;
     case 13: return 2;
     case 8: return 1;
     case 6: case 7: return 0;

@@ -186,6 +186,51 @@ __device__ __forceinline__ uint64_t position_key(uint64_t seed, uint64_t positio
   return mix64(mix64(seed) ^ position);
 }
 
+// e^z for z <= 0 within 2^-46 (relative): Cody-Waite reduction by ln 2 with
+// fused multiply-adds, a degree-11 Taylor polynomial on |r| <= 0.35
+// (truncation below 2^-47; 2^-46.7 is the largest error over 2e7
+// arguments), then ldexp. Not the reference's exp_d: used only where its
+// error is bounded above (the certified dense tail of smp_kernels.hip).
+__device__ __forceinline__ double exp_approx(double z) {
+  z = z >= -700.0 ? z : -700.0;  // (a NaN, from a padding lane, too: every value below stays defined)
+  const double t = __builtin_rint(z * 1.4426950408889634);
+  double r = __builtin_fma(-t, 0.6931471805599453, z);
+  r = __builtin_fma(-t, 2.3190468138462996e-17, r);
+  double p = 2.505210838544172e-08;                // 1/11!
+  p = __builtin_fma(p, r, 2.755731922398589e-07);  // 1/10!
+  p = __builtin_fma(p, r, 2.7557319223985893e-06); // 1/9!
+  p = __builtin_fma(p, r, 2.48015873015873e-05);   // 1/8!
+  p = __builtin_fma(p, r, 0.0001984126984126984);  // 1/7!
+  p = __builtin_fma(p, r, 0.001388888888888889);   // 1/6!
+  p = __builtin_fma(p, r, 0.008333333333333333);   // 1/5!
+  p = __builtin_fma(p, r, 0.041666666666666664);   // 1/4!
+  p = __builtin_fma(p, r, 0.16666666666666666);    // 1/3!
+  p = __builtin_fma(p, r, 0.5);
+  p = __builtin_fma(p, r, 1.0);
+  p = __builtin_fma(p, r, 1.0);
+  return __builtin_amdgcn_ldexp(p, (int)t);
+}
+
+// z + g of the version-3 draw (z = (l - M) / T, g the Gumbel noise of
+// gumbel_from_key) in binary32 arithmetic, within 1e-4 of the binary64 value
+// for |z| <= 40 and every uniform below 1: z to ~5e-6; -log u to ~1e-6
+// relative (from 1 - u, exact in binary64, by a series when u is near 1,
+// else from log of u); the outer log adds ~3e-6. 2.7e-6 is the largest
+// error over 2e7 uniforms, the endpoints included. At the uniform's upper
+// endpoint u = 1 both are +inf, so such an entry is never filtered out.
+__device__ __forceinline__ float score_approx(float zf, uint64_t pk, uint32_t token) {
+  const uint64_t h = mix64(pk ^ ((uint64_t)token * 0xd6e8feb86659fd93ull));
+  const double u = ((double)(h >> 11) + 0.5) * (1.0 / 9007199254740992.0);  // the reference's uniform
+  const float d = (float)(1.0 - u);  // exact for u >= 1/2
+  float l1;
+  if (d < 0.0625f) {
+    l1 = d * (1.0f + d * (0.5f + d * (0.33333334f + d * (0.25f + d * 0.2f))));
+  } else {
+    l1 = -logf((float)u);
+  }
+  return zf - logf(l1);
+}
+
 // Version-2 uniform; output_head_sampler.rs:196-197 (no +0.5).
 __device__ __forceinline__ double uniform_v2(uint64_t seed, uint64_t position) {
   return (double)(position_key(seed, position) >> 11) * (1.0 / 9007199254740992.0);

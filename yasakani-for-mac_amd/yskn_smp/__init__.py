@@ -644,9 +644,10 @@ def version() -> str:
 
 def pm_test(fn: int, inputs=None, base: int = 0, n: int = 0) -> np.ndarray:
     """yskn_smp_pm_test: one device primitive on host inputs (see
-    include/yskn_smp.h). fn 10/11/14 take u64 words (binary64 bits or
-    integers), 12 takes (seed, position, token) rows, 13 (seed, position)
-    rows, 6/7 the binary32 bit patterns base .. base + n - 1."""
+    include/yskn_smp.h). fn 10/11/14/15 take u64 words (binary64 bits or
+    integers), 12 takes (seed, position, token) rows, 16 (z binary32 bits,
+    position key, token) rows, 13 (seed, position) rows, 6/7 the binary32
+    bit patterns base .. base + n - 1."""
     L = load_library()
     if fn in (6, 7):
         out = np.zeros(n, np.uint32)
