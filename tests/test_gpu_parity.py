@@ -558,6 +558,73 @@ def test_large_launches_with_other_features():
     d.close()
 
 
+@pytest.mark.parametrize("case", range(30))
+def test_random_feature_combinations(case):
+    """Deterministic random combinations of row shape (padded, ragged),
+    element type, value distribution, per-row or shared parameters (top-k 1
+    to disabled, both versions, top-p, min-p, temperature), draws per row,
+    logprob and top lists, and penalties: ids, argmax, top-8 and logprob ids
+    against the oracle."""
+    rng = np.random.default_rng(5000 + case)
+    rows = int(rng.integers(1, 25))
+    V = int(rng.choice([1000, 4097, 20_000, 33_333, 60_000]))
+    pad = int(rng.choice([0, 3, 16]))
+    bf16 = bool(rng.random() < 0.3)
+    kind = int(rng.integers(0, 3))
+    sc = float(rng.uniform(0.5, 4.0))
+    if kind == 0:
+        x = sc * rng.standard_normal((rows, V))
+    elif kind == 1:
+        x = sc * rng.standard_t(3, (rows, V))
+    else:
+        x = np.round(sc * rng.standard_normal((rows, V)) * 16) / 16
+    x = x.astype(np.float32)
+    full = torch.zeros((rows, V + pad), dtype=torch.float32)
+    full[:, :V] = torch.from_numpy(x)
+    if bf16:
+        full = full.to(torch.bfloat16)
+        x = full[:, :V].float().numpy()
+    xt = full.to(DEV)[:, :V]
+    def params(r):
+        return SamplingParameters(temperature_milli=int(rng.integers(100, 3000)),
+                                  top_p_milli=int(rng.choice([300, 800, 950, 990, 1000])),
+                                  min_p_milli=int(rng.choice([0, 0, 10, 100])),
+                                  top_k=int(rng.choice([1, 5, 20, 64, 65, 300, 0])),
+                                  seed=int(rng.integers(0, 2**62)),
+                                  version=GUMBEL if rng.random() < 0.7 else INVERSE_CUMULATIVE)
+    shared = bool(rng.random() < 0.5)
+    sps = [params(0)] * rows if shared else [params(r) for r in range(rows)]
+    nd = int(rng.choice([1, 1, 3]))
+    n_lp = int(rng.choice([0, 8, 70]))
+    pen = bool(rng.random() < 0.3)
+    d = DeviceSampler(rows, V + pad, extended_top_k=True)
+    d.set_params(sps[0] if shared else sps)
+    pos = rng.integers(0, 2**40, (rows, nd)).astype(np.int64)
+    kw = dict(argmax=True, top8=True, n_logprobs=n_lp)
+    y = x
+    if pen:
+        hist = rng.integers(0, V, (rows, 1500)).astype(np.int32)
+        hl = rng.integers(0, 1501, rows).astype(np.int32)
+        sps = [SamplingParameters(temperature_milli=q.temperature_milli, top_p_milli=q.top_p_milli,
+                                  min_p_milli=q.min_p_milli, top_k=q.top_k, seed=q.seed, version=q.version,
+                                  repetition_penalty=1.1, presence_penalty=0.3, frequency_penalty=0.05)
+               for q in sps]
+        d.set_params(sps[0] if shared else sps)
+        kw.update(history=torch.from_numpy(hist).to(DEV), history_len=torch.from_numpy(hl).to(DEV))
+        y = np.stack([O.apply_penalties(x[r], hist[r, :hl[r]], 1.1, 0.3, 0.05) for r in range(rows)])
+    out = _run(d, xt, pos, **kw)
+    got = to_u32(out["ids"]).reshape(rows, nd)
+    ref = pmap(lambda r: list(O.sample_positions(y[r], pos[r].astype(np.uint64), oracle_params(sps[r], True))),
+               range(rows))
+    for r in range(rows):
+        assert list(got[r]) == ref[r], (case, r, sps[r])
+        assert int(to_u32(out["argmax"])[r]) == O.greedy(y[r]), (case, r)
+        assert list(to_u32(out["top8_ids"])[r]) == list(O.top_tokens(y[r], 8)), (case, r)
+        if n_lp:
+            assert list(to_u32(out["logprob_ids"])[r]) == list(O.top_logprobs(y[r], n_lp)[0]), (case, r)
+    d.close()
+
+
 # ---------------------------------------------------------------------------
 # the five workloads at full size
 # ---------------------------------------------------------------------------
