@@ -625,6 +625,39 @@ def test_random_feature_combinations(case):
     d.close()
 
 
+@pytest.mark.parametrize("case", range(20))
+def test_random_verify(case):
+    """Deterministic random verify calls: row count, vocabulary, parameters
+    (top-k 1 to disabled, both versions, min-p), drafts right up to a random
+    depth then wrong or right to the end, EOS ids drawn from the selections:
+    accepted, emitted, token and EOS flag against the oracle's accept loop."""
+    rng = np.random.default_rng(7000 + case)
+    M = int(rng.integers(1, 13))
+    V = int(rng.choice([2000, 30_001, 70_000]))
+    x = (float(rng.uniform(0.5, 3.0)) * rng.standard_normal((M, V))).astype(np.float32)
+    sp = SamplingParameters(temperature_milli=int(rng.integers(200, 2000)),
+                            top_p_milli=int(rng.choice([800, 950, 1000])),
+                            min_p_milli=int(rng.choice([0, 20])),
+                            top_k=int(rng.choice([1, 20, 64, 500, 0])), seed=int(rng.integers(0, 2**62)),
+                            version=GUMBEL if rng.random() < 0.7 else INVERSE_CUMULATIVE)
+    base = int(rng.integers(0, 2**40))
+    sel = [oracle_select(x[j], base + j + 1, sp, extension=True) for j in range(M)]
+    depth = int(rng.integers(0, M))
+    drafts = [sel[j] if j < depth or rng.random() < 0.3 else (sel[j] + 1) % V for j in range(M - 1)]
+    eos = [sel[int(rng.integers(0, M))]] if rng.random() < 0.3 else []
+    d = DeviceSampler(M, V, extended_top_k=True)
+    d.set_params(sp)
+    dt = torch.tensor(drafts if drafts else [0], dtype=torch.int32, device=DEV)
+    ids, res, _keep = d.verify(torch.from_numpy(x).to(DEV), dt, torch.tensor([base], device=DEV), eos)
+    d.sync()
+    osel, em, acc, stop = O.verify(x, drafts, base, oracle_params(sp, True), eos)
+    r = res.cpu().numpy().astype(np.int64)
+    assert (int(r[0]), int(r[1]), int(r[3])) == (acc, em, int(stop)), (case, M, depth)
+    assert int(r[2]) == int(osel[-1]), case
+    assert list(to_u32(ids)[:em]) == list(osel), case
+    d.close()
+
+
 # ---------------------------------------------------------------------------
 # the five workloads at full size
 # ---------------------------------------------------------------------------
