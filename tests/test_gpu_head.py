@@ -39,6 +39,30 @@ def _oracle_logits(acc, us, sums, tau, width=5120.0, eps=1e-6):
     return np.stack(out)
 
 
+def test_head_rows_with_top_k_disabled_take_the_certified_tail():
+    """Flat head rows with top-k disabled: every value is relevant, so the
+    finishing block re-forms the logits from the accumulators in its passes
+    over the row (certified tail). Ids, argmax and top-8 against the oracle."""
+    rows, V = 4, 60_000
+    acc, us, sums, tau = _head_inputs(rows, V, 99)
+    acc[:, :3] = acc[:, 3:6]  # no planted extreme values: a flat row
+    x = _oracle_logits(acc, us, sums, tau)
+    d = DeviceSampler(rows, V, extended_top_k=True)
+    sp = SamplingParameters(temperature_milli=1200, top_p_milli=920, min_p_milli=0, top_k=0, seed=5)
+    d.set_params(sp)
+    pos = np.arange(rows) * 5 + 3
+    t = lambda a: torch.from_numpy(a).to(DEV)
+    out = d.sample_head(t(acc), t(us), t(sums), t(tau), torch.tensor(pos, device=DEV), argmax=True, top8=True)
+    d.sync()
+    assert list(to_u32(out["ids"]).reshape(-1)) == pmap(
+        lambda r: oracle_select(x[r], int(pos[r]), sp, extension=True), range(rows))
+    assert list(to_u32(out["argmax"])) == [O.greedy(x[r]) for r in range(rows)]
+    for r in range(rows):
+        assert list(to_u32(out["top8_ids"])[r]) == list(O.top_tokens(x[r], 8))
+    assert d.stats()["certified_rows"] > 0
+    d.close()
+
+
 @pytest.mark.parametrize("rows,V", [(1, 151_936), (3, 1537), (8, 248_320), (16, 40_001)])
 def test_head_sampling_matches_the_oracle(rows, V):
     acc, us, sums, tau = _head_inputs(rows, V, rows * 7 + V)
