@@ -69,7 +69,7 @@ struct SegMeta {
   uint32_t theta;     // the segment's certified KB-th key: no larger than the row's
   double mass;        // sum of exp(l - mref) over the segment's mass terms
   float mref;         // reference point of that mass (-inf: no terms)
-  float pad2;
+  uint32_t part;      // the segment's share of the certified tail's first pass is in its slot
 };
 
 // Counters for profiling the path (cumulative since create).

@@ -1823,47 +1823,63 @@ __device__ __forceinline__ uint32_t compact_entries(const uint64_t* src, uint32_
 // first serial binary64 prefix S_j >= top_p * total and at the first w_j
 // below min-p, and draws over the kept prefix (output_head_sampler.rs
 // :136-190). Only the cut needs the order, and only near it:
-//  1. one pass over the row adds every relevant weight, and a count, into
-//     one of CB_NB buckets of z (bucket b holds the z with
-//     floor(-z CB_NB / 37.5) = b, the last bucket everything below: an
-//     interval of the candidate order), and finds the largest key whose
-//     weight is below min-p (the first candidate min-p drops);
+//  1. every relevant weight, and a count, is added into one of CB_NB buckets
+//     of an absolute grid of the values (grid_bucket: an interval of the
+//     candidate order each). A segmented row's blocks add their shares
+//     before they hand over (cert_share: weights relative to the segment's
+//     maximum, buckets relative to its grid cell); the finishing block
+//     shifts and scales them into place. Otherwise the finishing block reads
+//     the row once for this;
 //  2. a second pass collects the bucket in which the running bucket sums
-//     cross top_p * total and the buckets that hold the first KB candidates
-//     (the lists), and sums the weights of the min-p bucket's kept
-//     candidates; both collections are sorted in LDS;
+//     cross top_p * total, the buckets that hold the first KB candidates
+//     (the lists) and the bucket that holds the min-p threshold, finds the
+//     largest key below that bucket, and writes out the entries kept
+//     whichever cut holds (those before both buckets); the cut and head
+//     collections are sorted in LDS;
 //  3. the sums are not the reference's serial binary64 sum: other order,
-//     weights from exp_approx of z' = (l - M) * (1 / T) instead of exp_d of
-//     z = (l - M) / T (within 2^-44 of w each for |z| <= 40: 2^-46 from the
-//     polynomial, 2^-45.7 from z). Every prefix
-//     or total formed here is within
-//     E = 2^-53 R (4n + 2 CB_NB + 2 CAP + 64) + 2^-43 R
-//     of the serial value it stands for (R the total, n the candidates:
-//     each serial addition, each bucket and scan addition, each addition of
-//     the walk through the collected bucket and the top-p product round by
-//     at most 2^-53 R; the weights add at most 2^-44 R). A cut is taken only
-//     when every compare it rests on holds with a margin of 2E, and min-p's
-//     only when no weight lies within 2^-40 of min-p (relative); otherwise,
-//     or when a collection does not fit, the function returns 0 and the
-//     caller sorts the row (the exact path);
+//     weights from exp_approx (within 2^-46 relative) of z' = (l - M) * (1 / T)
+//     or of the segment's (l - Ms) * (1 / T) times exp_approx((Ms - M) * (1 / T))
+//     instead of exp_d of z = (l - M) / T: within 2^-43 of w each for
+//     |z| <= 40. Every prefix or total formed here is within
+//     E = 2^-53 R (4n + 2 CB_NB + 2 CAP + 64) + 2^-42 R
+//     of the serial value it stands for (R the total, n the counted
+//     elements: each serial addition, each bucket, merge and scan addition,
+//     each addition of the walk through the collected bucket and the top-p
+//     product round by at most 2^-53 R; the weights add at most 2^-43 R). A
+//     cut is taken only when every compare it rests on holds with a margin
+//     of 2E, and min-p's only when no weight of the threshold bucket lies
+//     within 2^-40 (relative) of min-p and the threshold is not within 10^-6
+//     grid steps of a bucket edge (every weight outside that bucket is then
+//     at least 9e-9 away from min-p, relative); otherwise, or when a
+//     collection does not fit, the function returns 0 and the caller sorts
+//     the row (the exact path);
 //  4. the kept candidates are a prefix of the order: the second pass writes
-//     out those before the cut bucket, the sorted cut bucket adds its part.
-//     A draw takes the largest binary32 score (within SC_TOL of z + g,
-//     score_approx) over them, then the exact binary64 z + g of the entries
-//     within 2 SC_TOL of it, ties to the earlier candidate (the reference's
-//     strict > in candidate order).
+//     out those before the collected buckets, the sorted cut bucket (top-p
+//     cut) or the threshold bucket (min-p cut) adds its part. A draw takes
+//     the largest binary32 score (within SC_TOL of z + g, score_approx)
+//     over them, then the exact binary64 z + g of the entries within
+//     2 SC_TOL of it, ties to the earlier candidate (the reference's strict
+//     > in candidate order).
 // Passes over the row keep the next tile's loads in flight while a tile is
 // processed. The total is also summed in a second order; a difference
-// beyond the bound fails the certification too. On success fl.cand holds the first KB candidates, sorted,
-// out_ids the draws, and the return value is the number of relevant
-// elements. Block-wide.
+// beyond the bound fails the certification too. On success fl.cand holds
+// the first KB candidates, sorted, out_ids the draws, and the return value
+// is the number of counted elements. Block-wide.
 // ---------------------------------------------------------------------------
-constexpr int CB_NB = 4096;     // z buckets of the certified tail
-constexpr float SC_TOL = 1e-4f;  // bound on |score_approx - (z + g)|
-constexpr int DRB = 8;           // entries per thread and round of the draw passes
+constexpr int CB_NB = 4096;       // buckets of the certified tail
+constexpr float SC_TOL = 1e-4f;   // bound on |score_approx - (z + g)|
+constexpr int DRB = 8;            // entries per thread and round of the draw passes
+constexpr int BCAP = 2016;        // entries of the min-p threshold bucket kept in LDS
+constexpr int64_t CSLOT = CB_NB + CB_NB / 2 + 8;  // doubles of a segment's share in the row's scratch
 
-__device__ __forceinline__ uint32_t cert_bucket(double z) {
-  const double t = -z * ((double)CB_NB / 37.5);
+// Bucket of value l on the absolute grid of step 1/c: F(M) - F(l) with
+// F(x) = floor(x c) (fm = F(M)), the values CB_NB - 1 or more steps below in
+// the last bucket (a NaN too). With c = CB_NB / (37.5 T) every relevant value
+// lands in 0..CB_NB - 1; the bucket does not decrease along the candidate
+// order, and a segment's bucket relative to its own F(Ms) is this one shifted
+// by F(M) - F(Ms).
+__device__ __forceinline__ uint32_t grid_bucket(double fm, double l, double c) {
+  const double t = fm - floor(l * c);
   return t < (double)(CB_NB - 1) ? (uint32_t)t : (uint32_t)(CB_NB - 1);
 }
 
@@ -1880,13 +1896,14 @@ __device__ __forceinline__ void draw_load(const uint64_t* da, int64_t nk, int64_
 struct CertShared {
   double R;            // sum of the bucket sums
   double a_cut;        // bucket sums before the cut bucket
-  double a_fb;         // bucket sums before the bucket of the first candidate min-p drops
+  double a_star;       // bucket sums before the min-p threshold bucket
   double p_lo, p_hi;   // prefix before and through the cut candidate
-  uint32_t n;          // relevant elements
-  uint32_t bcut, ccut; // cut bucket, candidates before it
-  uint32_t btop, ctop; // last bucket of the head, candidates through it
+  uint32_t n;          // counted elements
+  uint32_t bcut, ccut; // cut bucket, elements before it
+  uint32_t btop, ctop; // last bucket of the head, elements through it
   uint32_t ncut, ntop; // entries collected
-  uint32_t nk;         // kept entries compacted
+  uint32_t nb;         // entries of the threshold bucket collected
+  uint32_t nk;         // kept entries written
   int32_t j0;          // cut position in the sorted cut bucket (-1: not found)
 };
 
@@ -1896,16 +1913,16 @@ struct CertShared {
 // keys only where they are used (cert_keys), so that the loads of the next
 // tile stay in flight while a tile is processed.
 template <int DT, bool PEN, int PER>
-__device__ __forceinline__ void cert_load(const RowCtx& rc, int V, int64_t base, uint32_t (&b)[PER]) {
+__device__ __forceinline__ void cert_load(const RowCtx& rc, int64_t V, int64_t base, uint32_t (&b)[PER]) {
 #pragma unroll
   for (int q = 0; q < PER; ++q) {
     const int64_t i = base + (int64_t)q * NT + (int64_t)threadIdx.x;
-    b[q] = value_bits<DT, PEN>(rc, i < V ? i : (int64_t)V - 1);
+    b[q] = value_bits<DT, PEN>(rc, i < V ? i : V - 1);
   }
 }
-// Keys of those elements (0 past the row).
+// Keys of those elements (0 past the end).
 template <int PER>
-__device__ __forceinline__ void cert_keys(int V, int64_t base, const uint32_t (&b)[PER], uint32_t (&k)[PER]) {
+__device__ __forceinline__ void cert_keys(int64_t V, int64_t base, const uint32_t (&b)[PER], uint32_t (&k)[PER]) {
 #pragma unroll
   for (int q = 0; q < PER; ++q) {
     const int64_t i = base + (int64_t)q * NT + (int64_t)threadIdx.x;
@@ -1913,70 +1930,151 @@ __device__ __forceinline__ void cert_keys(int V, int64_t base, const uint32_t (&
   }
 }
 
+// Step 1 over elements [e0, e1) with weights relative to maximum Mw and
+// buckets relative to fw = F(Mw), relevant = key >= trel, into hw / hc
+// (LDS, cleared here). Returns the thread's sum of the weights.
+template <int DT, bool PEN>
+__device__ __forceinline__ double cert_pass1(const RowCtx& rc, int64_t e0, int64_t e1, float Mw, double fw, double c,
+                                             double invT, uint32_t trel, double* hw, uint32_t* hc) {
+  constexpr int P1 = 8;
+  const int tid = threadIdx.x;
+  for (int i = tid; i < CB_NB; i += NT) {
+    hw[i] = 0.0;
+    hc[i] = 0u;
+  }
+  __syncthreads();
+  const double Mwd = (double)Mw;
+  double ws = 0.0;
+  uint32_t nx[P1];
+  cert_load<DT, PEN, P1>(rc, e1, e0, nx);
+  for (int64_t base = e0; base < e1; base += (int64_t)NT * P1) {
+    uint32_t kk[P1];
+    cert_keys<P1>(e1, base, nx, kk);
+    if (base + (int64_t)NT * P1 < e1) cert_load<DT, PEN, P1>(rc, e1, base + (int64_t)NT * P1, nx);
+    // every element's weight and bucket first, outside the branches, so
+    // that the elements' dependent chains interleave
+    double wv[P1];
+    uint32_t bv[P1];
+#pragma unroll
+    for (int q = 0; q < P1; ++q) {
+      const double l = (double)key2f(kk[q]);
+      wv[q] = exp_approx((l - Mwd) * invT);
+      bv[q] = grid_bucket(fw, l, c);
+      ws += kk[q] >= trel ? wv[q] : 0.0;
+    }
+#pragma unroll
+    for (int q = 0; q < P1; ++q) {
+      if (kk[q] >= trel) {
+        atomicAdd(&hw[bv[q]], wv[q]);
+        atomicAdd(&hc[bv[q]], 1u);
+      }
+    }
+  }
+  __syncthreads();
+  return ws;
+}
+
+// A segment of a row headed for the certified tail (its export overflowed)
+// adds its share of step 1 before it hands over: its elements relevant to
+// its own maximum Ms (a superset of the row's relevant ones: the extra ones
+// lie CB_NB - 1 or more grid steps below M, in the last bucket), weights
+// relative to Ms, buckets relative to F(Ms), into its slot of the row's
+// scratch. Returns false, writing nothing, when the slot does not fit the
+// scratch or the grid is too fine for exact integer steps. Block-wide.
+template <int DT, bool PEN>
+__device__ __forceinline__ bool cert_share(const SmpArgs& A, const DevParams& P, const RowCtx& rc, int row, int seg,
+                                           int nseg, float Ms, int64_t e0, int64_t e1, RowLds& fl, double* redd) {
+  const double T = P.temperature, invT = 1.0 / T, c = (double)CB_NB / (37.5 * T);
+  const double msc = (double)Ms * c;
+  if ((int64_t)nseg * CSLOT > A.dense_ld || !(fabs(msc) < 0x1p30)) return false;
+  double* hw = (double*)fl.buf;
+  uint32_t* hc = (uint32_t*)(fl.buf + CB_NB);
+  __syncthreads();  // (the export read the append buffer)
+  double ws = cert_pass1<DT, PEN>(rc, e0, e1, Ms, floor(msc), c, invT, relevance_key(Ms, T), hw, hc);
+  ws = block_sum_f64(ws, redd);
+  double* slot = A.dense_w + (int64_t)row * A.dense_ld + (int64_t)seg * CSLOT;
+  uint32_t* sc = (uint32_t*)(slot + CB_NB);
+  for (int i = threadIdx.x; i < CB_NB; i += NT) {
+    slot[i] = hw[i];
+    sc[i] = hc[i];
+  }
+  if (threadIdx.x == 0) slot[CB_NB + CB_NB / 2] = ws;
+  __syncthreads();
+  return true;
+}
+
 template <int DT, bool PEN>
 __device__ __forceinline__ int64_t dense_certified(const SmpArgs& A, const DevParams& P, const RowCtx& rc,
-                                                   int row, float M, uint32_t trel, const RowPlan& plan,
+                                                   int row, int nseg, float M, uint32_t trel, const RowPlan& plan,
                                                    RowLds& fl, double* redd, uint64_t* redu) {
-  constexpr int P1 = 8, P2 = 16;
+  constexpr int P2 = 16;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int V = A.V;
   const double T = P.temperature;
   const double invT = 1.0 / T;
   const double Md = (double)M;
+  const double c = (double)CB_NB / (37.5 * T);
+  const double fm = floor(Md * c);
   double* hw = (double*)fl.buf;                            // [CB_NB] bucket sums
   uint32_t* hc = (uint32_t*)(fl.buf + CB_NB);              // [CB_NB] bucket counts
   CertShared* cs = (CertShared*)(fl.buf + CB_NB + CB_NB / 2);
+  uint64_t* bkt = fl.buf + CB_NB + CB_NB / 2 + 32;         // [BCAP] the min-p threshold bucket
   uint64_t* top = fl.cand;                                 // the head buckets
   uint64_t* cut = (uint64_t*)fl.w;                         // the cut bucket
-  for (int i = tid; i < CB_NB; i += NT) {
-    hw[i] = 0.0;
-    hc[i] = 0u;
+  static_assert(CB_NB + CB_NB / 2 + 32 + BCAP <= BUFCAP && sizeof(CertShared) <= 32 * 8, "certified tail LDS layout");
+  // the min-p threshold l* = M + T log(min_p) and its bucket
+  const bool minp = P.min_p > 0.0;
+  const double lstar = Md + T * log(P.min_p > 0.0 ? P.min_p : 1.0);
+  const double lsc = lstar * c;
+  const double fr = lsc - floor(lsc);
+  const uint32_t bstar = minp ? grid_bucket(fm, lstar, c) : (uint32_t)CB_NB;
+  if (!(fabs(Md * c) < 0x1p30) || (minp && (!(fabs(lsc) < 0x1p30) || fr < 1e-6 || fr > 1.0 - 1e-6 ||
+                                            bstar >= (uint32_t)(CB_NB - 2))))
+    return 0;  // (uniform)
+  // 1. the bucket sums: the segments' shares, shifted and scaled, or one pass
+  bool merged = false;
+  if (nseg > 1) {
+    const SegMeta* mt = A.exp_meta + (int64_t)row * nseg;
+    bool all = true;
+    for (int s = 0; s < nseg; ++s) all = all && mt[s].part != 0u && mt[s].mkey != 0u;
+    merged = all;
+  }
+  double wrel = 0.0;
+  if (merged) {
+    const SegMeta* mt = A.exp_meta + (int64_t)row * nseg;
+    for (int i = tid; i < CB_NB; i += NT) {
+      hw[i] = 0.0;
+      hc[i] = 0u;
+    }
+    __syncthreads();
+    for (int s = 0; s < nseg; ++s) {
+      const double Ms = (double)key2f(mt[s].mkey);
+      const double o = fm - floor(Ms * c);  // >= 0: Ms <= M
+      const double f = exp_approx((Ms - Md) * invT);
+      const double* slot = A.dense_w + (int64_t)row * A.dense_ld + (int64_t)s * CSLOT;
+      const uint32_t* sc = (const uint32_t*)(slot + CB_NB);
+      for (int j = tid; j < CB_NB; j += NT) {
+        const uint32_t cv = sc[j];
+        if (cv) {
+          const double bt = (double)j + o;
+          const uint32_t b = bt < (double)(CB_NB - 1) ? (uint32_t)bt : (uint32_t)(CB_NB - 1);
+          atomicAdd(&hw[b], f * slot[j]);
+          atomicAdd(&hc[b], cv);
+        }
+      }
+      wrel += f * slot[CB_NB + CB_NB / 2];  // (every thread: the same sum)
+    }
+    __syncthreads();
+  } else {
+    wrel = cert_pass1<DT, PEN>(rc, 0, V, M, fm, c, invT, trel, hw, hc);
+    wrel = block_sum_f64(wrel, redd);  // the total once more, in another order (a cross-check)
   }
   if (tid == 0) {
     cs->ncut = 0u;
     cs->ntop = 0u;
+    cs->nb = 0u;
     cs->nk = 0u;
   }
-  __syncthreads();
-  // 1. bucket sums and counts; the largest key whose weight is below min-p
-  const double mp_lo = P.min_p * (1.0 - 0x1p-40), mp_hi = P.min_p * (1.0 + 0x1p-40);
-  uint32_t kfb = 0u;
-  bool amb = false;  // a weight too close to min-p to decide
-  double wrel = 0.0;
-  {
-    uint32_t nx[P1];
-    cert_load<DT, PEN, P1>(rc, V, 0, nx);
-    for (int64_t base = 0; base < V; base += (int64_t)NT * P1) {
-      uint32_t kk[P1];
-      cert_keys<P1>(V, base, nx, kk);
-      if (base + (int64_t)NT * P1 < V) cert_load<DT, PEN, P1>(rc, V, base + (int64_t)NT * P1, nx);
-      // every element's weight and bucket first, outside the branches, so
-      // that the elements' dependent chains interleave
-      double wv[P1];
-      uint32_t bv[P1];
-#pragma unroll
-      for (int q = 0; q < P1; ++q) {
-        const double z = ((double)key2f(kk[q]) - Md) * invT;
-        wv[q] = exp_approx(z);
-        bv[q] = cert_bucket(z);
-        wrel += kk[q] >= trel ? wv[q] : 0.0;
-      }
-#pragma unroll
-      for (int q = 0; q < P1; ++q) {
-        if (kk[q] >= trel) {
-          atomicAdd(&hw[bv[q]], wv[q]);
-          atomicAdd(&hc[bv[q]], 1u);
-          if (wv[q] < mp_lo && kk[q] > kfb) kfb = kk[q];
-          amb |= wv[q] >= mp_lo && wv[q] <= mp_hi;
-        }
-      }
-    }
-  }
-  kfb = (uint32_t)block_max_u64((uint64_t)kfb, redu);
-  amb = block_max_u64(amb ? 1ull : 0ull, redu) != 0ull;
-  wrel = block_sum_f64(wrel, redd);  // the total once more, in another order (a cross-check)
-  const uint32_t bfb = kfb ? cert_bucket(((double)key2f(kfb) - Md) * invT) : (uint32_t)CB_NB;
-  __syncthreads();
   // the running sums over the buckets (wave 0; lane l owns buckets 64l..64l+63)
   if (wave == 0) {
     const int b0 = lane * 64;
@@ -2001,9 +2099,9 @@ __device__ __forceinline__ int64_t dense_certified(const SmpArgs& A, const DevPa
     const uint32_t n = (uint32_t)__shfl((int)ec, 63);
     const double tau = P.top_p * R;
     double a = ew - sw;
-    uint32_t c = ec - sc;
+    uint32_t cn = ec - sc;
     int fcut = -1, ftop = -1;
-    double acut = 0.0, afb = 0.0;
+    double acut = 0.0, astar = 0.0;
     uint32_t ccut = 0u, ctop = 0u;
     for (int i = 0; i < 64; ++i) {
       const double wb = hw[b0 + i];
@@ -2011,22 +2109,22 @@ __device__ __forceinline__ int64_t dense_certified(const SmpArgs& A, const DevPa
       if (fcut < 0 && a + wb >= tau) {
         fcut = b0 + i;
         acut = a;
-        ccut = c;
+        ccut = cn;
       }
-      if (ftop < 0 && c + cb >= (uint32_t)plan.KB) {
+      if (ftop < 0 && cn + cb >= (uint32_t)plan.KB) {
         ftop = b0 + i;
-        ctop = c + cb;
+        ctop = cn + cb;
       }
-      if ((uint32_t)(b0 + i) == bfb) afb = a;
+      if ((uint32_t)(b0 + i) == bstar) astar = a;
       a += wb;
-      c += cb;
+      cn += cb;
     }
     const uint64_t mc = __ballot(fcut >= 0), mt = __ballot(ftop >= 0);
     const int lc = mc ? (int)__builtin_ctzll(mc) : 0, lt = mt ? (int)__builtin_ctzll(mt) : 0;
     const int bcut = __shfl(fcut, lc), btop = __shfl(ftop, lt);
     const double a_cut = __shfl(acut, lc);
     const uint32_t c_cut = (uint32_t)__shfl((int)ccut, lc), c_top = (uint32_t)__shfl((int)ctop, lt);
-    if ((uint32_t)lane == (bfb >> 6) && bfb < (uint32_t)CB_NB) cs->a_fb = afb;
+    if ((uint32_t)lane == (bstar >> 6) && bstar < (uint32_t)CB_NB) cs->a_star = astar;
     if (lane == 0) {
       cs->R = R;
       cs->n = n;
@@ -2040,19 +2138,23 @@ __device__ __forceinline__ int64_t dense_certified(const SmpArgs& A, const DevPa
   __syncthreads();
   const uint32_t n = cs->n, bcut = cs->bcut, btop = cs->btop;
   // the candidates are the relevant elements (top-k at or above their
-  // count); the cut bucket and the head must fit the LDS collections
-  if (amb || n == 0u || plan.k_eff < (int64_t)n || bcut >= (uint32_t)CB_NB || btop >= (uint32_t)CB_NB ||
-      hc[bcut] > (uint32_t)CAP || cs->ctop > (uint32_t)CAP) {
+  // count); the collected buckets lie above the last one (which may hold
+  // counted elements below the relevance cut) and fit the LDS collections
+  if (n == 0u || plan.k_eff < (int64_t)n || bcut >= (uint32_t)(CB_NB - 1) || btop >= (uint32_t)(CB_NB - 1) ||
+      hc[bcut] > (uint32_t)CAP || cs->ctop > (uint32_t)CAP ||
+      (minp && bstar != bcut && hc[bstar] > (uint32_t)BCAP)) {
     __syncthreads();
     return 0;
   }
-  // 2. collect the cut bucket and the head; sum what min-p keeps of its
-  // bucket; write out the entries kept whichever cut holds (every kept entry
-  // outside the cut bucket: with the min-p cut, S_(m-1) < top_p * total - E
-  // puts every kept entry at or before the cut bucket; with the top-p cut,
-  // every entry before the cut bucket precedes the cut and so lies above kfb)
+  // 2. collect the cut bucket, the head and the threshold bucket; the
+  // largest key below the threshold bucket; write out the entries before
+  // both collected buckets (kept whichever cut holds: with the min-p cut,
+  // S_(m-1) < top_p * total - E puts every kept entry at or before the cut
+  // bucket and the kept set ends in the threshold bucket; with the top-p cut
+  // the kept set ends in the cut bucket, at or before the threshold bucket)
   uint64_t* da = A.dense_a + (int64_t)row * A.dense_ld;
-  double pfb = 0.0;
+  const uint32_t bw = bcut < bstar ? bcut : bstar;
+  uint32_t kbelow = 0u;
   {
     uint32_t nx[P2];
     cert_load<DT, PEN, P2>(rc, V, 0, nx);
@@ -2062,11 +2164,10 @@ __device__ __forceinline__ int64_t dense_certified(const SmpArgs& A, const DevPa
       if (base + (int64_t)NT * P2 < V) cert_load<DT, PEN, P2>(rc, V, base + (int64_t)NT * P2, nx);
 #pragma unroll
       for (int q = 0; q < P2; ++q) {
-        const double z = ((double)key2f(kk[q]) - Md) * invT;
-        const uint32_t b = cert_bucket(z);
+        const uint32_t b = grid_bucket(fm, (double)key2f(kk[q]), c);
         const uint64_t e = pack(kk[q], (uint32_t)(base + (int64_t)q * NT + tid));
-        // kept whichever cut holds: before the cut bucket and above kfb
-        const bool wr = kk[q] >= trel && b < bcut && kk[q] > kfb;
+        const bool rel = kk[q] >= trel;
+        const bool wr = rel && b < bw;
         const uint64_t wm = __ballot(wr);
         if (wm) {
           const int first = (int)__builtin_ctzll(wm);
@@ -2075,11 +2176,14 @@ __device__ __forceinline__ int64_t dense_certified(const SmpArgs& A, const DevPa
           s0 = (uint32_t)__builtin_amdgcn_readlane((int)s0, first);
           if (wr) da[s0 + lanes_below(wm)] = e;
         }
-        if (kk[q] >= trel) {
-          if (b == bfb && kk[q] > kfb) pfb += exp_approx(z);
+        if (rel) {
+          if (b > bstar && kk[q] > kbelow) kbelow = kk[q];
           if (b == bcut) {
             const uint32_t s = atomicAdd(&cs->ncut, 1u);
             if (s < (uint32_t)CAP) cut[s] = e;
+          } else if (b == bstar) {
+            const uint32_t s = atomicAdd(&cs->nb, 1u);
+            if (s < (uint32_t)BCAP) bkt[s] = e;
           }
           if (b <= btop) {
             const uint32_t s = atomicAdd(&cs->ntop, 1u);
@@ -2089,30 +2193,58 @@ __device__ __forceinline__ int64_t dense_certified(const SmpArgs& A, const DevPa
       }
     }
   }
-  pfb = block_sum_f64(pfb, redd);
+  kbelow = (uint32_t)block_max_u64((uint64_t)kbelow, redu);
   __syncthreads();
   const uint32_t ncut = cs->ncut, ntop = cs->ntop;
-  if (ncut != hc[bcut] || ntop != cs->ctop) {
+  const uint32_t nb = bstar == bcut ? ncut : cs->nb;
+  const uint64_t* const sb = bstar == bcut ? cut : bkt;  // the threshold bucket's entries
+  if (ncut != hc[bcut] || ntop != cs->ctop || (minp && bstar != bcut && nb != hc[bstar])) {
     __syncthreads();
     return 0;
   }
   __syncthreads();
   sort_desc(top, (int)ntop);
   sort_desc(cut, (int)ncut);
+  // the first candidate min-p drops: the largest key below min-p in the
+  // threshold bucket, else the largest key below that bucket
+  const double mp_lo = P.min_p * (1.0 - 0x1p-40), mp_hi = P.min_p * (1.0 + 0x1p-40);
+  uint32_t kfb = 0u;
+  bool amb = false;
+  if (minp) {
+    for (uint32_t j = (uint32_t)tid; j < nb; j += NT) {
+      const uint32_t k = pk_key(sb[j]);
+      const double w = exp_approx(((double)key2f(k) - Md) * invT);
+      if (w < mp_lo && k > kfb) kfb = k;
+      amb |= w >= mp_lo && w <= mp_hi;
+    }
+    kfb = (uint32_t)block_max_u64((uint64_t)kfb, redu);
+    amb = block_max_u64(amb ? 1ull : 0ull, redu) != 0ull;
+    if (kfb == 0u) kfb = kbelow;
+  }
+  double pfb = 0.0;  // the threshold bucket's weights above kfb
+  if (minp && kfb) {
+    for (uint32_t j = (uint32_t)tid; j < nb; j += NT) {
+      const uint32_t k = pk_key(sb[j]);
+      if (k > kfb) pfb += exp_approx(((double)key2f(k) - Md) * invT);
+    }
+  }
+  pfb = block_sum_f64(pfb, redd);
   // the cut bucket's weights, in candidate order
   for (uint32_t j = (uint32_t)tid; j < ncut; j += NT) hw[j] = exp_approx(((double)key2f(pk_key(cut[j])) - Md) * invT);
   __syncthreads();
   // 3. the cut, certified
   const double R = cs->R;
-  const double marg = 2.0 * ((R * 0x1p-53) * (4.0 * (double)n + 2.0 * CB_NB + 2.0 * CAP + 64.0) + R * 0x1p-43);
+  const double marg = 2.0 * ((R * 0x1p-53) * (4.0 * (double)n + 2.0 * CB_NB + 2.0 * CAP + 64.0) + R * 0x1p-42);
   const double tau = P.top_p * R;
   int mode = 0;  // 0: not certified, 1: min-p cut, 2: top-p cut
-  if (kfb) {
-    const double pm = cs->a_fb + pfb;  // the weights of the candidates min-p keeps
-    if (pm < tau - marg) mode = 1;
-    else if (pm >= tau + marg) mode = 2;
+  if (amb) {
+    mode = 0;
+  } else if (kfb) {
+    const double pm = cs->a_star + pfb;  // the weights of the candidates min-p keeps
+    if (pm < tau - marg && bstar <= bcut) mode = 1;
+    else if (pm >= tau + marg && bcut <= bstar) mode = 2;
   } else {
-    mode = 2;
+    mode = (!minp || bcut <= bstar) ? 2 : 0;
   }
   if (mode == 2) {
     if (wave == 0) {
@@ -2156,12 +2288,15 @@ __device__ __forceinline__ int64_t dense_certified(const SmpArgs& A, const DevPa
     __syncthreads();
     return 0;
   }
-  // 4. the kept entries of the cut bucket join those written in pass 2:
-  // with the top-p cut its first j0 + 1, with the min-p cut those above kfb
+  // 4. the kept entries of the last bucket join those written in pass 2:
+  // with the top-p cut the cut bucket's first j0 + 1, with the min-p cut the
+  // threshold bucket's entries above kfb
   {
     const int32_t j0 = mode == 2 ? cs->j0 : -1;
-    for (uint32_t j = (uint32_t)tid; j < ncut; j += NT) {
-      const uint64_t e = cut[j];
+    const uint32_t m4 = mode == 2 ? ncut : nb;
+    const uint64_t* const s4 = mode == 2 ? cut : sb;
+    for (uint32_t j = (uint32_t)tid; j < m4; j += NT) {
+      const uint64_t e = s4[j];
       if (mode == 2 ? (int32_t)j <= j0 : pk_key(e) > kfb) da[atomicAdd(&cs->nk, 1u)] = e;
     }
   }
@@ -2690,6 +2825,16 @@ __global__ __launch_bounds__(NT) void smp_row(SmpArgs Ain) {
     } else {
       nx = EXP_CAP + 1u;  // reservations outran the spill share
     }
+    // an overflow sends the row to the dense path: a row headed for the
+    // certified tail gets this segment's share of its first pass now
+    bool part = false;
+    if constexpr (CERT) {
+      if (nx > (uint32_t)EXP_CAP && mk_s != 0u && !fdense && plan.sampled && plan.need_rel &&
+          P.version == YSKN_V3 && !P.zcheck) {
+        const int64_t e1 = (int64_t)ce * WSEG < (int64_t)V ? (int64_t)ce * WSEG : (int64_t)V;
+        part = cert_share<DT, PEN>(A, P, rc, row, seg, nseg, key2f(mk_s), (int64_t)cb * WSEG, e1, fl, red_f64);
+      }
+    }
     if (wave == 0) {
       // the segment's mass relative to its largest wave reference point
       const float mr = lane < NW ? s_mref[lane] : -__builtin_inff();
@@ -2706,6 +2851,7 @@ __global__ __launch_bounds__(NT) void smp_row(SmpArgs Ain) {
         m.theta = theta;
         m.mass = ms;
         m.mref = mr_s;
+        m.part = part ? 1u : 0u;
       }
     }
     // release: the barrier completes every wave's stores of the export and
@@ -2928,7 +3074,7 @@ __global__ __launch_bounds__(NT) void smp_row(SmpArgs Ain) {
       int64_t nc = 0;
       if constexpr (CERT) {
         if (!fdense && plan.sampled && plan.need_rel && P.version == YSKN_V3 && !P.zcheck)
-          nc = dense_certified<DT, PEN>(A, P, rc, row, M, trel, plan, fl, red_f64, red_u64);
+          nc = dense_certified<DT, PEN>(A, P, rc, row, nseg, M, trel, plan, fl, red_f64, red_u64);
       }
       drawn = nc > 0;
       if (drawn) ncand = nc;
