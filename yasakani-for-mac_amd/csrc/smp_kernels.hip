@@ -1879,8 +1879,8 @@ constexpr int64_t CSLOT = CB_NB + CB_NB / 2 + 8;  // doubles of a segment's shar
 // order, and a segment's bucket relative to its own F(Ms) is this one shifted
 // by F(M) - F(Ms).
 __device__ __forceinline__ uint32_t grid_bucket(double fm, double l, double c) {
-  const double t = fm - floor(l * c);
-  return t < (double)(CB_NB - 1) ? (uint32_t)t : (uint32_t)(CB_NB - 1);
+  const double t = fm - floor(l * c);  // >= 0: no value exceeds the maximum
+  return t < (double)(CB_NB - 1) ? (t > 0.0 ? (uint32_t)t : 0u) : (uint32_t)(CB_NB - 1);
 }
 
 // Entries j0 + q * NT + tid of the compacted kept set (clamped: all DRB
@@ -2056,8 +2056,8 @@ __device__ __forceinline__ int64_t dense_certified(const SmpArgs& A, const DevPa
       for (int j = tid; j < CB_NB; j += NT) {
         const uint32_t cv = sc[j];
         if (cv) {
-          const double bt = (double)j + o;
-          const uint32_t b = bt < (double)(CB_NB - 1) ? (uint32_t)bt : (uint32_t)(CB_NB - 1);
+          const double bt = (double)j + o;  // >= 0: o = F(M) - F(Ms) >= 0
+          const uint32_t b = bt < (double)(CB_NB - 1) ? (bt > 0.0 ? (uint32_t)bt : 0u) : (uint32_t)(CB_NB - 1);
           atomicAdd(&hw[b], f * slot[j]);
           atomicAdd(&hc[b], cv);
         }
