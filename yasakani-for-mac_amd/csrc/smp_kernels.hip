@@ -1782,7 +1782,10 @@ __device__ __forceinline__ void chunk_filter(int c, int lane, const uint32_t (&k
 
 // Order-free parallel compaction: appends to dst the entries of src[0, n)
 // with key >= thr, at most cap in all; *ctr counts every qualifying entry
-// (reset first if `reset`). Returns *ctr (every thread). Block-wide.
+// (reset first if `reset`). Returns *ctr (every thread). With STOP a wave
+// stops once the count has passed cap (the caller only needs to know that
+// it did; the count returned is then some value above cap). Block-wide.
+template <bool STOP = false>
 __device__ __forceinline__ uint32_t compact_entries(const uint64_t* src, uint32_t n, uint64_t* dst,
                                                     uint32_t cap, uint32_t thr, uint32_t* ctr, bool reset) {
   const int tid = threadIdx.x, lane = tid & 63;
@@ -1792,6 +1795,9 @@ __device__ __forceinline__ uint32_t compact_entries(const uint64_t* src, uint32_
   }
   __syncthreads();
   for (uint32_t i0 = 0; i0 < n; i0 += NT) {
+    if (STOP && __builtin_amdgcn_readfirstlane(
+                    (int)__hip_atomic_load(ctr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP)) > (int)cap)
+      break;
     const uint32_t i = i0 + (uint32_t)tid;
     uint64_t e = 0;
     bool keep = false;
@@ -1871,6 +1877,7 @@ constexpr float SC_TOL = 1e-4f;   // bound on |score_approx - (z + g)|
 constexpr int DRB = 8;            // entries per thread and round of the draw passes
 constexpr int BCAP = 2016;        // entries of the min-p threshold bucket kept in LDS
 constexpr int64_t CSLOT = CB_NB + CB_NB / 2 + 8;  // doubles of a segment's share in the row's scratch
+static_assert(CB_NB % NT == 0, "bucket array in whole rounds of the block");
 
 // Bucket of value l on the absolute grid of step 1/c: F(M) - F(l) with
 // F(x) = floor(x c) (fm = F(M)), the values CB_NB - 1 or more steps below in
@@ -2053,13 +2060,21 @@ __device__ __forceinline__ int64_t dense_certified(const SmpArgs& A, const DevPa
       const double f = exp_approx((Ms - Md) * invT);
       const double* slot = A.dense_w + (int64_t)row * A.dense_ld + (int64_t)s * CSLOT;
       const uint32_t* sc = (const uint32_t*)(slot + CB_NB);
-      for (int j = tid; j < CB_NB; j += NT) {
-        const uint32_t cv = sc[j];
-        if (cv) {
-          const double bt = (double)j + o;  // >= 0: o = F(M) - F(Ms) >= 0
+      constexpr int MQ = CB_NB / NT;  // a thread's buckets of the share: all loads in flight together
+      uint32_t cv[MQ];
+      double hv[MQ];
+#pragma unroll
+      for (int q = 0; q < MQ; ++q) {
+        cv[q] = sc[q * NT + tid];
+        hv[q] = slot[q * NT + tid];
+      }
+#pragma unroll
+      for (int q = 0; q < MQ; ++q) {
+        if (cv[q]) {
+          const double bt = (double)(q * NT + tid) + o;  // >= 0: o = F(M) - F(Ms) >= 0
           const uint32_t b = bt < (double)(CB_NB - 1) ? (bt > 0.0 ? (uint32_t)bt : 0u) : (uint32_t)(CB_NB - 1);
-          atomicAdd(&hw[b], f * slot[j]);
-          atomicAdd(&hc[b], cv);
+          atomicAdd(&hw[b], f * hv[q]);
+          atomicAdd(&hc[b], cv[q]);
         }
       }
       wrel += f * slot[CB_NB + CB_NB / 2];  // (every thread: the same sum)
@@ -2817,11 +2832,12 @@ __global__ __launch_bounds__(NT) void smp_row(SmpArgs Ain) {
     uint64_t* const xc = A.exp_cand + ((int64_t)row * nseg + seg) * EXP_CAP;
     const uint32_t cnt = sh.count;
     uint32_t nx;
+    // (an export past EXP_CAP is of no use: the compaction stops there)
     if (cnt <= (uint32_t)BUFCAP) {
-      nx = compact_entries(fl.buf, cnt, xc, EXP_CAP, theta_s, &sh.ctr, true);
+      nx = compact_entries<true>(fl.buf, cnt, xc, EXP_CAP, theta_s, &sh.ctr, true);
     } else if ((int64_t)(cnt - (uint32_t)BUFCAP) <= spill_share) {
-      compact_entries(fl.buf, BUFCAP, xc, EXP_CAP, theta_s, &sh.ctr, true);
-      nx = compact_entries(spill, cnt - (uint32_t)BUFCAP, xc, EXP_CAP, theta_s, &sh.ctr, false);
+      compact_entries<true>(fl.buf, BUFCAP, xc, EXP_CAP, theta_s, &sh.ctr, true);
+      nx = compact_entries<true>(spill, cnt - (uint32_t)BUFCAP, xc, EXP_CAP, theta_s, &sh.ctr, false);
     } else {
       nx = EXP_CAP + 1u;  // reservations outran the spill share
     }
