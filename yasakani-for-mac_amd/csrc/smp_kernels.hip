@@ -2321,8 +2321,10 @@ __device__ __forceinline__ int64_t dense_certified(const SmpArgs& A, const DevPa
   const int nd = A.mode == MODE_VERIFY ? 1 : A.n_draws;
   for (int d = 0; d < nd; ++d) {
     const uint64_t pk = position_key(P.seed, position_of(A, row, d));
-    // the largest binary32 score ...
-    float smax = -__builtin_inff();
+    // the largest binary32 score (and each thread's two largest, with the
+    // entry of the first) ...
+    float s1 = -__builtin_inff(), s2 = -__builtin_inff();
+    uint64_t e1 = 0ull;
     uint64_t nv[DRB];  // the next round's entries, in flight while a round is scored
     if (nk > 0) draw_load(da, nk, 0, nv);
     for (int64_t j0 = 0; j0 < nk; j0 += (int64_t)NT * DRB) {
@@ -2334,9 +2336,14 @@ __device__ __forceinline__ int64_t dense_certified(const SmpArgs& A, const DevPa
       for (int q = 0; q < DRB; ++q) {
         const uint64_t e = ev[q];
         const float s = score_approx((key2f(pk_key(e)) - Mf) * invTf, pk, pk_id(e));
-        smax = (j0 + (int64_t)q * NT + tid < nk && s > smax) ? s : smax;
+        const float sv = j0 + (int64_t)q * NT + tid < nk ? s : -__builtin_inff();
+        const bool up = sv > s1;
+        s2 = up ? s1 : (sv > s2 ? sv : s2);
+        e1 = up ? e : e1;
+        s1 = up ? sv : s1;
       }
     }
+    float smax = s1;
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) {
       const float t = __shfl_xor(smax, o);
@@ -2349,11 +2356,18 @@ __device__ __forceinline__ int64_t dense_certified(const SmpArgs& A, const DevPa
 #pragma unroll
     for (int q = 1; q < NW; ++q) sm = redd[q] > sm ? redd[q] : sm;
     const float thr = (float)sm - 2.0f * SC_TOL;
-    // ... then the exact z + g of the entries within 2 SC_TOL of it
+    // ... then the exact z + g of the entries within 2 SC_TOL of it: each
+    // thread's first when no thread has a second there (the common case),
+    // else every entry again
     double best = -__builtin_inf();
     uint64_t be = 0ull;
-    if (nk > 0) draw_load(da, nk, 0, nv);
-    for (int64_t j0 = 0; j0 < nk; j0 += (int64_t)NT * DRB) {
+    const bool again = block_max_u64(s2 >= thr ? 1ull : 0ull, redu) != 0ull;
+    if (!again && s1 >= thr && s1 != -__builtin_inff()) {
+      best = ((double)key2f(pk_key(e1)) - Md) / T + gumbel_from_key(pk, pk_id(e1));
+      be = e1;
+    }
+    if (again && nk > 0) draw_load(da, nk, 0, nv);
+    for (int64_t j0 = 0; again && j0 < nk; j0 += (int64_t)NT * DRB) {
       uint64_t ev[DRB];
 #pragma unroll
       for (int q = 0; q < DRB; ++q) ev[q] = nv[q];
