@@ -2177,20 +2177,29 @@ __device__ __forceinline__ int64_t dense_certified(const SmpArgs& A, const DevPa
       uint32_t kk[P2];
       cert_keys<P2>(V, base, nx, kk);
       if (base + (int64_t)NT * P2 < V) cert_load<DT, PEN, P2>(rc, V, base + (int64_t)NT * P2, nx);
+      // the tile's written entries reserved by one LDS atomic per wave (the
+      // whole wave is active), then stored in element order
+      uint32_t bq[P2];
+      uint64_t wq[P2];
+      uint32_t nw = 0u;
 #pragma unroll
       for (int q = 0; q < P2; ++q) {
-        const uint32_t b = grid_bucket(fm, (double)key2f(kk[q]), c);
+        bq[q] = grid_bucket(fm, (double)key2f(kk[q]), c);
+        wq[q] = __ballot(kk[q] >= trel && bq[q] < bw);
+        nw += (uint32_t)__popcll(wq[q]);
+      }
+      uint32_t s0 = 0u;
+      if (nw) {
+        if (lane == 0) s0 = atomicAdd(&cs->nk, nw);
+        s0 = (uint32_t)__builtin_amdgcn_readfirstlane((int)s0);
+      }
+#pragma unroll
+      for (int q = 0; q < P2; ++q) {
+        const uint32_t b = bq[q];
         const uint64_t e = pack(kk[q], (uint32_t)(base + (int64_t)q * NT + tid));
         const bool rel = kk[q] >= trel;
-        const bool wr = rel && b < bw;
-        const uint64_t wm = __ballot(wr);
-        if (wm) {
-          const int first = (int)__builtin_ctzll(wm);
-          uint32_t s0 = 0u;
-          if (lane == first) s0 = atomicAdd(&cs->nk, (uint32_t)__popcll(wm));
-          s0 = (uint32_t)__builtin_amdgcn_readlane((int)s0, first);
-          if (wr) da[s0 + lanes_below(wm)] = e;
-        }
+        if ((wq[q] >> lane) & 1ull) da[s0 + lanes_below(wq[q])] = e;
+        s0 += (uint32_t)__popcll(wq[q]);
         if (rel) {
           if (b > bstar && kk[q] > kbelow) kbelow = kk[q];
           if (b == bcut) {
