@@ -1912,7 +1912,22 @@ struct CertShared {
   uint32_t nb;         // entries of the threshold bucket collected
   uint32_t nk;         // kept entries written
   int32_t j0;          // cut position in the sorted cut bucket (-1: not found)
+  uint32_t kb[6];      // key bounds of the second pass (lower_key)
 };
+
+// The smallest key in [lo, f2key(+inf)] whose value lies in bucket x or a
+// lower one. Over non-NaN values the bucket does not increase with the key
+// (grid_bucket is F(M) - floor(l c), clamped), so the keys of buckets <= x
+// are exactly those at or above this one; +inf is in bucket 0.
+__device__ __forceinline__ uint32_t lower_key(double fm, double c, uint32_t x, uint32_t lo) {
+  uint32_t hi = 0xff800000u;  // f2key(+inf)
+  while (lo < hi) {
+    const uint32_t mid = lo + (hi - lo) / 2u;
+    if (grid_bucket(fm, (double)key2f(mid), c) <= x) hi = mid;
+    else lo = mid + 1u;
+  }
+  return lo;
+}
 
 // Raw bits of elements base + q * NT + tid. Every load is issued, at a
 // clamped index, so that all PER are in flight together (a load behind a
@@ -2170,6 +2185,20 @@ __device__ __forceinline__ int64_t dense_certified(const SmpArgs& A, const DevPa
   uint64_t* da = A.dense_a + (int64_t)row * A.dense_ld;
   const uint32_t bw = bcut < bstar ? bcut : bstar;
   uint32_t kbelow = 0u;
+  // Every bucket set the pass asks about is an interval of relevant keys
+  // (lower_key; no value here is NaN or infinite: such a row is flagged
+  // non-finite and does not reach this tail), so elements are classified by
+  // key compares alone: kb[0] written (b < bw), [kb[1], kb[2]) the cut
+  // bucket, [kb[3], kb[4]) the threshold bucket (below kb[3]: b > bstar),
+  // kb[5] the head (b <= btop). A bound of a bucket below 0 is no key.
+  if (tid < 6) {
+    const int64_t x = tid == 0 ? (int64_t)bw - 1 : tid == 1 ? (int64_t)bcut : tid == 2 ? (int64_t)bcut - 1
+                    : tid == 3 ? (int64_t)bstar : tid == 4 ? (int64_t)bstar - 1 : (int64_t)btop;
+    cs->kb[tid] = x < 0 ? 0xffffffffu : lower_key(fm, c, (uint32_t)x, trel);
+  }
+  __syncthreads();
+  const uint32_t kw = cs->kb[0], kc0 = cs->kb[1], kc1 = cs->kb[2], ks0 = cs->kb[3], ks1 = cs->kb[4],
+                 kt = cs->kb[5];
   {
     uint32_t nx[P2];
     cert_load<DT, PEN, P2>(rc, V, 0, nx);
@@ -2179,13 +2208,11 @@ __device__ __forceinline__ int64_t dense_certified(const SmpArgs& A, const DevPa
       if (base + (int64_t)NT * P2 < V) cert_load<DT, PEN, P2>(rc, V, base + (int64_t)NT * P2, nx);
       // the tile's written entries reserved by one LDS atomic per wave (the
       // whole wave is active), then stored in element order
-      uint32_t bq[P2];
       uint64_t wq[P2];
       uint32_t nw = 0u;
 #pragma unroll
       for (int q = 0; q < P2; ++q) {
-        bq[q] = grid_bucket(fm, (double)key2f(kk[q]), c);
-        wq[q] = __ballot(kk[q] >= trel && bq[q] < bw);
+        wq[q] = __ballot(kk[q] >= kw);  // (kw >= trel: written entries are relevant)
         nw += (uint32_t)__popcll(wq[q]);
       }
       uint32_t s0 = 0u;
@@ -2195,21 +2222,20 @@ __device__ __forceinline__ int64_t dense_certified(const SmpArgs& A, const DevPa
       }
 #pragma unroll
       for (int q = 0; q < P2; ++q) {
-        const uint32_t b = bq[q];
-        const uint64_t e = pack(kk[q], (uint32_t)(base + (int64_t)q * NT + tid));
-        const bool rel = kk[q] >= trel;
+        const uint32_t k = kk[q];
+        const uint64_t e = pack(k, (uint32_t)(base + (int64_t)q * NT + tid));
         if ((wq[q] >> lane) & 1ull) da[s0 + lanes_below(wq[q])] = e;
         s0 += (uint32_t)__popcll(wq[q]);
-        if (rel) {
-          if (b > bstar && kk[q] > kbelow) kbelow = kk[q];
-          if (b == bcut) {
+        if (k >= trel) {
+          if (k < ks0 && k > kbelow) kbelow = k;  // b > bstar
+          if (k >= kc0 && k < kc1) {
             const uint32_t s = atomicAdd(&cs->ncut, 1u);
             if (s < (uint32_t)CAP) cut[s] = e;
-          } else if (b == bstar) {
+          } else if (k >= ks0 && k < ks1) {
             const uint32_t s = atomicAdd(&cs->nb, 1u);
             if (s < (uint32_t)BCAP) bkt[s] = e;
           }
-          if (b <= btop) {
+          if (k >= kt) {
             const uint32_t s = atomicAdd(&cs->ntop, 1u);
             if (s < (uint32_t)CAP) top[s] = e;
           }
@@ -2227,8 +2253,12 @@ __device__ __forceinline__ int64_t dense_certified(const SmpArgs& A, const DevPa
     return 0;
   }
   __syncthreads();
-  sort_desc(top, (int)ntop);
-  sort_desc(cut, (int)ncut);
+  // (the bucket sums are not read again: their array is the small sorts'
+  // scratch)
+  if (ntop <= (uint32_t)NT) sort_desc_small(top, (uint64_t*)hw, (int)ntop);
+  else sort_desc(top, (int)ntop);
+  if (ncut <= (uint32_t)NT) sort_desc_small(cut, (uint64_t*)hw, (int)ncut);
+  else sort_desc(cut, (int)ncut);
   // the first candidate min-p drops: the largest key below min-p in the
   // threshold bucket, else the largest key below that bucket
   const double mp_lo = P.min_p * (1.0 - 0x1p-40), mp_hi = P.min_p * (1.0 + 0x1p-40);
