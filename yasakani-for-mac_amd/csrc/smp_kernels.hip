@@ -2200,12 +2200,8 @@ __device__ __forceinline__ int64_t dense_certified(const SmpArgs& A, const DevPa
   const uint32_t kw = cs->kb[0], kc0 = cs->kb[1], kc1 = cs->kb[2], ks0 = cs->kb[3], ks1 = cs->kb[4],
                  kt = cs->kb[5];
   {
-    uint32_t nx[P2];
-    cert_load<DT, PEN, P2>(rc, V, 0, nx);
-    for (int64_t base = 0; base < V; base += (int64_t)NT * P2) {
-      uint32_t kk[P2];
-      cert_keys<P2>(V, base, nx, kk);
-      if (base + (int64_t)NT * P2 < V) cert_load<DT, PEN, P2>(rc, V, base + (int64_t)NT * P2, nx);
+    // one tile of NT * P2 elements (keys 0 past the end: not relevant)
+    auto tile = [&](const uint32_t (&kk)[P2], int64_t base) {
       // the tile's written entries reserved by one LDS atomic per wave (the
       // whole wave is active), then stored in element order
       uint64_t wq[P2];
@@ -2241,6 +2237,20 @@ __device__ __forceinline__ int64_t dense_certified(const SmpArgs& A, const DevPa
           }
         }
       }
+    };
+    // two tiles in flight (loads at clamped indices: in range past the end)
+    constexpr int64_t TL = (int64_t)NT * P2;
+    uint32_t la[P2], lb[P2];
+    cert_load<DT, PEN, P2>(rc, V, 0, la);
+    cert_load<DT, PEN, P2>(rc, V, TL, lb);
+    for (int64_t base = 0; base < V; base += 2 * TL) {
+      uint32_t kk[P2];
+      cert_keys<P2>(V, base, la, kk);
+      if (base + 2 * TL < V) cert_load<DT, PEN, P2>(rc, V, base + 2 * TL, la);
+      tile(kk, base);
+      cert_keys<P2>(V, base + TL, lb, kk);
+      if (base + 3 * TL < V) cert_load<DT, PEN, P2>(rc, V, base + 3 * TL, lb);
+      tile(kk, base + TL);
     }
   }
   kbelow = (uint32_t)block_max_u64((uint64_t)kbelow, redu);
