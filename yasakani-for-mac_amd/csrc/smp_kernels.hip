@@ -1330,6 +1330,49 @@ __device__ void sort_desc_small(uint64_t* a, uint64_t* b, int n) {
   __syncthreads();
 }
 
+// Descending sort of NT < n <= 2 NT packed candidates in LDS `a` (distinct
+// values, nonzero), `b` LDS scratch of n entries: each wave sorts two
+// 64-element runs in registers, and every element's final position is its
+// position in its run plus, for each other run, the number of larger
+// elements there (binary search), as in sort_desc_small.
+__device__ void sort_desc_runs2(uint64_t* a, uint64_t* b, int n) {
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int runs = (n + 63) / 64;  // 9..16
+  uint64_t v[2];
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const int run = wave + h * NW;
+    const int i = run * 64 + lane;
+    v[h] = 0ull;
+    if (run < runs) {
+      v[h] = wave_sort_desc_u64(i < n ? a[i] : 0ull);
+      a[i] = v[h];  // run `run`, descending, zeros (absent) last
+    }
+  }
+  __syncthreads();
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const int run = wave + h * NW;
+    if (run < runs && v[h] != 0ull) {
+      int rank = lane;
+      for (int w = 0; w < runs; ++w) {
+        if (w == run) continue;
+        const uint64_t* r = a + w * 64;
+        int lo = 0, hi = 64;  // first position whose value is below v
+        while (lo < hi) {
+          const int mid = (lo + hi) >> 1;
+          if (r[mid] > v[h]) lo = mid + 1; else hi = mid;
+        }
+        rank += lo;
+      }
+      b[rank] = v[h];
+    }
+  }
+  __syncthreads();
+  for (int i = tid; i < n; i += NT) a[i] = b[i];
+  __syncthreads();
+}
+
 // The exact k-th largest key among n >= k packed entries in LDS: four 8-bit
 // radix passes from the top. Each wave adds its lanes' digits with one LDS
 // atomic per distinct digit (ballot-matched peers), and every wave picks the
@@ -2266,8 +2309,10 @@ __device__ __forceinline__ int64_t dense_certified(const SmpArgs& A, const DevPa
   // (the bucket sums are not read again: their array is the small sorts'
   // scratch)
   if (ntop <= (uint32_t)NT) sort_desc_small(top, (uint64_t*)hw, (int)ntop);
+  else if (ntop <= 2u * NT) sort_desc_runs2(top, (uint64_t*)hw, (int)ntop);
   else sort_desc(top, (int)ntop);
   if (ncut <= (uint32_t)NT) sort_desc_small(cut, (uint64_t*)hw, (int)ncut);
+  else if (ncut <= 2u * NT) sort_desc_runs2(cut, (uint64_t*)hw, (int)ncut);
   else sort_desc(cut, (int)ncut);
   // the first candidate min-p drops: the largest key below min-p in the
   // threshold bucket, else the largest key below that bucket
